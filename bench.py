@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of decide's prefill GEMM path on one MI355X.
+
+Workload ("C2"): the fused MLP block at M = 603,
+d_model 2560, d_ff 9216, fp16 operands, fp32 accumulation:
+  (1) gate|up  [603×2560]·[18432×2560]ᵀ with the SwiGLU epilogue → fp16 [603, 9216]
+  (2) down     [603×9216]·[2560×9216]ᵀ with the AddF32 epilogue (3: residual add fused)
+One step = one pass of the block over the batch. Inputs are synthetic (seeded
+Gaussians, X ~ N(0, 1), W ~ N(0, 0.02)) and resident in HBM before timing.
+Three copies of the weights (423 MB > the 256 MB Infinity Cache) are used in
+rotation so every step streams its weights from HBM.
+
+Prints ONE JSON line. `value` = the block's algorithmic TFLOP/s
+(2·M·N·K summed over both GEMMs ÷ time per step). `roofline` describes the
+dominant kernel (gate|up): its algorithmic TFLOP ÷ its average launch time,
+timed with HIP events on the stream it runs on, against 2.5 PFLOP/s dense
+fp16 MFMA. `cpu_baseline` times the oracle (decide's cpu_ref::gemm_nt
+restated in C: f64 sums, single thread) on a bounded sample of rows.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16 MFMA (256 CU × 2.4 GHz × 4096 flop/clk)
+PEAK_HBM_GBS = 8000.0
+
+M, D, F = 603, 2560, 9216
+WEIGHT_COPIES = 3
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--report", action="store_true", help="also print per-shape GEMM timings to stderr")
+    return ap.parse_args()
+
+
+def flops(m, n, k):
+    return 2.0 * m * n * k
+
+
+def traffic_from_profile():
+    """HBM bytes per gate|up launch measured with rocprofv3 --pmc (profiles/), if recorded."""
+    path = os.path.join(ROOT, "profiles", "gateup_m603_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(seconds: float):
+    """The oracle's faithful restatement of cpu_ref::gemm_nt (single-threaded, f64 sums) over a
+    bounded sample of the C2 block's rows, reported in TFLOP/s like the GPU value."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as orc
+    from decide_amd import synth
+
+    x = synth.normal_f16(synth.seed_for(21), (M, D), 1.0).astype(np.float32)
+    wgu = synth.normal_f16(synth.seed_for(22), (2 * F, D), 0.02).astype(np.float32)
+    wdn = synth.normal_f16(synth.seed_for(23), (D, F), 0.02).astype(np.float32)
+    rows_done, elapsed, chunk = 0, 0.0, 8
+    while rows_done < M and (elapsed < seconds or rows_done == 0):
+        xs = x[rows_done:rows_done + chunk]
+        t0 = time.perf_counter()
+        y = orc.gemm_nt(xs, wgu)
+        h = orc.f16_round(orc.swiglu_interleaved(y))
+        orc.gemm_nt(h, wdn)
+        elapsed += time.perf_counter() - t0
+        rows_done += len(xs)
+    work = flops(rows_done, 2 * F, D) + flops(rows_done, D, F)
+    return {
+        "value": work / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{rows_done} of {M} rows of the C2 MLP block (gate|up + SwiGLU + down), "
+                  f"oracle cpu_ref::gemm_nt restatement, f64 sums, 1 thread, {elapsed:.1f} s",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not implemented)"}))
+        sys.exit(2)
+
+    import torch
+
+    from decide_amd import synth
+    from decide_amd.kernels import Epilogue, Kernels, fill_normal_f16
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU"}))
+        sys.exit(1)
+    dev = torch.device("cuda")
+    k = Kernels()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    # ---- resident inputs
+    x = torch.from_numpy(synth.normal_f16(synth.seed_for(21), (M, D), 1.0)).to(dev)
+    x0 = torch.from_numpy(synth.normal_f32(synth.seed_for(24), (M, D), 1.0)).to(dev)
+    wgu = [torch.empty((2 * F, D), dtype=torch.float16, device=dev) for _ in range(WEIGHT_COPIES)]
+    wdn = [torch.empty((D, F), dtype=torch.float16, device=dev) for _ in range(WEIGHT_COPIES)]
+    for i in range(WEIGHT_COPIES):
+        fill_normal_f16(k.ctx, stream, (wgu[i], 0), wgu[i].numel(), synth.seed_for(22) + 1000 * i, 0.02)
+        fill_normal_f16(k.ctx, stream, (wdn[i], 0), wdn[i].numel(), synth.seed_for(23) + 1000 * i, 0.02)
+    mlp = torch.empty((M, F), dtype=torch.float16, device=dev)
+    res = x0.clone()
+    k.gemm.warm_up(stream, max_m=M)
+    base_loaded = k.gemm.fast_pipelines()
+
+    def step(i, ev=None):
+        c = i % WEIGHT_COPIES
+        if ev is not None:
+            ev[0].record()
+        k.gemm.gemm(stream, (x, 0), (wgu[c], 0), (mlp, 0), M, 2 * F, D, D, D, F, Epilogue.SwigluF16)
+        if ev is not None:
+            ev[1].record()
+        k.gemm.gemm(stream, (mlp, 0), (wdn[c], 0), (res, 0), M, D, F, F, F, D, Epilogue.AddF32)
+        if ev is not None:
+            ev[2].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # ---- timed region: whole steps, and per-kernel event pairs on the same stream
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        step(i, evs[i])
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    total_ms = start.elapsed_time(stop)
+    ms_per_step = total_ms / args.steps
+    gu_ms = np.array([e[0].elapsed_time(e[1]) for e in evs])
+    dn_ms = np.array([e[1].elapsed_time(e[2]) for e in evs])
+    assert k.gemm.fast_pipelines() == base_loaded, "a kernel was loaded inside the timed region"
+    assert torch.isfinite(res).all().item() and torch.isfinite(mlp.float()).all().item()
+
+    f_gu, f_dn = flops(M, 2 * F, D), flops(M, D, F)
+    value = (f_gu + f_dn) / (ms_per_step * 1e-3) / 1e12
+    gu_tflops = f_gu / (gu_ms.mean() * 1e-3) / 1e12
+    plan_gu = k.gemm.plan(M, 2 * F, D, Epilogue.SwigluF16)
+    plan_dn = k.gemm.plan(M, D, F, Epilogue.AddF32)
+
+    out = {
+        "metric": "prefill GEMM TFLOP/s (C2 fused MLP block, M=603) + % fp16 MFMA peak",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded Gaussians, X~N(0,1), W~N(0,0.02); 3 weight copies rotated)",
+        "config": {
+            "workload": "C2: fused MLP block, gate|up GEMM + SwiGLU epilogue, down GEMM + residual add",
+            "M": M, "d_model": D, "d_ff": F,
+            "gateup": {"m": M, "n": 2 * F, "k": D, "epi": "SwigluF16", "plan": plan_gu},
+            "down": {"m": M, "n": D, "k": F, "epi": "AddF32", "plan": plan_dn},
+        },
+        "pct_mfma_peak": round(100.0 * value / PEAK_FP16_TFLOPS, 2),
+        "kernels": {
+            "gateup_us_mean": round(gu_ms.mean() * 1e3, 2),
+            "gateup_us_p50": round(float(np.median(gu_ms)) * 1e3, 2),
+            "gateup_tflops": round(gu_tflops, 2),
+            "down_us_mean": round(dn_ms.mean() * 1e3, 2),
+            "down_tflops": round(f_dn / (dn_ms.mean() * 1e-3) / 1e12, 2),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_tile (gate|up, SwiGLU epilogue)",
+            "achieved": round(gu_tflops, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gu_tflops / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic_from_profile(),
+            "algorithmic_flops_per_launch": f_gu,
+            "algorithmic_bytes_per_launch": 2 * M * D + 2 * 2 * F * D + 2 * M * F,
+        },
+        "wall_ms_timed_region": round(wall_ms, 2),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,132 @@
+"""ctypes binding of libdecide_hip.so, the C ABI declared in include/decide_hip.h.
+
+The library is loaded from this package directory only (it is built in-tree by
+``decide_amd/csrc/Makefile``); a missing or stale library raises instead of
+falling back to anything else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_uint16, c_uint32, c_uint64, c_void_p
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdecide_hip.so")
+
+DH_OK = 0
+DH_EINVAL = 1
+DH_ELAUNCH = 2
+DH_ENOMEM = 3
+DH_EDEVICE = 4
+
+DH_GEMM_REFERENCE = 1
+
+
+class DhGemmMember(ctypes.Structure):
+    """``dh_gemm_member`` (include/decide_hip.h)."""
+
+    _fields_ = [
+        ("w", c_void_p),
+        ("y", c_void_p),
+        ("ldw", c_uint32),
+        ("ldy", c_uint32),
+        ("n", c_uint32),
+        ("epi", c_uint32),
+    ]
+
+
+class DhGemmPlan(ctypes.Structure):
+    """``dh_gemm_plan`` (include/decide_hip.h)."""
+
+    _fields_ = [
+        ("variant", c_uint32),
+        ("bm", c_uint32),
+        ("bn", c_uint32),
+        ("waves", c_uint32),
+        ("splits", c_uint32),
+        ("workgroups", c_uint32),
+        ("ws_bytes", c_uint64),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/decide_hip.h declares.
+PROTOTYPES = {
+    "dh_ctx_create": (c_int, [c_uint32, POINTER(c_void_p)]),
+    "dh_ctx_destroy": (None, [c_void_p]),
+    "dh_last_error": (c_char_p, []),
+    "dh_version": (c_char_p, []),
+    "dh_warm_up": (c_int, [c_void_p, c_void_p, c_uint32]),
+    "dh_variants_loaded": (c_uint32, [c_void_p]),
+    "dh_gemm_nt": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_uint32, c_uint32,
+         c_uint32, c_uint32],
+    ),
+    "dh_gemm_nt_grouped": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(DhGemmMember), c_uint32],
+    ),
+    "dh_gemm_plan_for": (c_int, [c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, POINTER(DhGemmPlan)]),
+    "dh_gemm_force": (c_int, [c_void_p, c_uint32, c_uint32]),
+    "dh_gemm_variant_count": (c_uint32, []),
+    "dh_gemm_variant_info": (
+        c_int,
+        [c_uint32, POINTER(c_uint32), POINTER(c_uint32), POINTER(c_uint32), POINTER(c_uint32)],
+    ),
+    "dh_gather_rows_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+    "dh_gather_rows_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+    "dh_final_head": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
+         c_uint32, c_float],
+    ),
+    "dh_rmsnorm_rows": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
+         c_uint32, c_float],
+    ),
+    "dh_fill_normal_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_float]),
+    "dh_interleave_gate_up": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
+    "dh_deinterleave_q_gate": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
+    "dh_bf16_to_f16": (c_int, [c_void_p, c_void_p, c_uint64, POINTER(c_uint64)]),
+}
+
+_lib = None
+
+
+class DecideHipError(RuntimeError):
+    """A DH_E* status from the library, with its message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library (loaded once). Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built: run `make -C decide_amd/csrc` (or __graft_entry__.build()). "
+            "There is no fallback path."
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().dh_last_error().decode()
+
+
+def check(rc: int) -> None:
+    """Raise DecideHipError for a non-DH_OK status."""
+    if rc != DH_OK:
+        raise DecideHipError(rc, last_error())

@@ -1,0 +1,377 @@
+// The C ABI (include/decide_hip.h): contract checks, planning, launches.
+//
+// Contract checks restate decide's Gemm::gemm asserts
+// (crates/decide-engine/src/kernels/gemm.rs:140-163) and Norm::rmsnorm's
+// (kernels/norm.rs:27), returning DH_EINVAL with the same wording instead of
+// panicking; nothing is launched after a failed check.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/decide_hip.h"
+#include "dh_kernels.h"
+#include "plan.h"
+
+struct dh_ctx {
+  uint32_t flags = 0;
+  int device = 0;
+  std::mutex ws_lock;
+  float* ws = nullptr;
+  uint64_t ws_bytes = 0;
+  uint64_t ws_cap = 512ull << 20;  // split-K workspace ceiling
+  int forced_variant = -1;
+  uint32_t forced_splits = 0;
+  std::atomic<uint64_t> used{0};  // bit per distinct kernel launched
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+// Kernel ids for dh_variants_loaded beyond the tile menu.
+enum : int { kKidReduce = 48, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill };
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return DH_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(DH_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+void mark(dh_ctx* c, int kid) { c->used.fetch_or(1ull << kid, std::memory_order_relaxed); }
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// gemm.rs:140-144 and 159-163.
+int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const void* y, uint32_t ldy, uint32_t m,
+               uint32_t n, uint32_t k, uint32_t epi) {
+  if (epi > 3u) return fail(DH_EINVAL, "gemm: epilogue %u is not one of 0..3", epi);
+  if (n % 32 != 0 || k % 32 != 0)
+    return fail(DH_EINVAL, "gemm: N = %u and K = %u must be multiples of 32", n, k);
+  if (m < 1) return fail(DH_EINVAL, "gemm: M must be at least 1");
+  if (ldx < k || ldw < k)
+    return fail(DH_EINVAL, "gemm: row strides ldx = %u, ldw = %u must cover K = %u", ldx, ldw, k);
+  const uint32_t y_cols = epi == DH_EPI_SWIGLU_F16 ? n / 2 : n;
+  if (ldy < y_cols) return fail(DH_EINVAL, "gemm: row stride ldy = %u must cover the %u output columns", ldy, y_cols);
+  if (ldx % 8 != 0 || ldw % 8 != 0)
+    return fail(DH_EINVAL, "gemm (fast): ldx = %u and ldw = %u must be multiples of 8", ldx, ldw);
+  if (!aligned(x, 16) || !aligned(w, 16))
+    return fail(DH_EINVAL, "gemm (fast): x/w addresses %p/%p must be multiples of 16", x, w);
+  if (ldy % 2 != 0) return fail(DH_EINVAL, "gemm (fast): ldy = %u must be even", ldy);
+  const uintptr_t y_align = (epi == DH_EPI_STORE_F32 || epi == DH_EPI_ADD_F32) ? 8 : 4;
+  if (!aligned(y, y_align)) return fail(DH_EINVAL, "gemm (fast): y address %p must be a multiple of %u", y, (unsigned)y_align);
+  if (!x || !w || !y) return fail(DH_EINVAL, "gemm: null operand");
+  return DH_OK;
+}
+
+int ensure_ws(dh_ctx* c, uint64_t bytes) {
+  std::lock_guard<std::mutex> g(c->ws_lock);
+  if (bytes <= c->ws_bytes) return DH_OK;
+  if (c->ws) {
+    hipError_t e = hipFree(c->ws);
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+    if (e != hipSuccess) return fail(DH_EDEVICE, "split-K workspace: hipFree: %s", hipGetErrorString(e));
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return fail(DH_ENOMEM, "split-K workspace of %llu bytes: %s", (unsigned long long)bytes,
+                                   hipGetErrorString(e));
+  c->ws = (float*)p;
+  c->ws_bytes = bytes;
+  return DH_OK;
+}
+
+dh::Plan choose_plan(const dh_ctx* c, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
+  if (c && c->forced_variant >= 0) {
+    return dh::plan_make(c->forced_variant, std::max(1u, c->forced_splits), m, n, k, epi);
+  }
+  return dh::plan_gemm(m, n, k, epi, c ? c->ws_cap : (512ull << 20));
+}
+
+int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint32_t ldx, uint32_t m, uint32_t k,
+                const dh_gemm_member* mem, uint32_t count) {
+  dh::TileArgs a{};
+  a.x = (const _Float16*)x;
+  a.ldx = ldx;
+  a.m = m;
+  a.k = k;
+  a.mtiles = p.mtiles;
+  a.splits = p.splits;
+  a.kps = p.kps;
+  a.count = count;
+  const dh::VariantInfo vi = dh::variant_info(p.variant);
+  uint32_t stripes = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    a.mem[i].w = (const _Float16*)mem[i].w;
+    a.mem[i].y = mem[i].y;
+    a.mem[i].ldw = mem[i].ldw;
+    a.mem[i].ldy = mem[i].ldy;
+    a.mem[i].n = mem[i].n;
+    a.mem[i].epi = mem[i].epi;
+    a.mem[i].stripe_begin = stripes;
+    stripes += (mem[i].n + vi.bn() - 1) / vi.bn();
+  }
+  a.nstripes = stripes;
+  if (p.splits > 1) {
+    if (count != 1) return fail(DH_EINVAL, "gemm: split-K needs a single member");
+    int rc = ensure_ws(c, p.ws_bytes);
+    if (rc != DH_OK) return rc;
+    a.ws = c->ws;
+  }
+  const uint32_t grid = p.mtiles * stripes * p.splits;
+  mark(c, p.variant);
+  int rc = hip_status(dh::launch_tile(p.variant, a, grid, s), "gemm tile kernel launch");
+  if (rc != DH_OK || p.splits == 1) return rc;
+  mark(c, kKidReduce);
+  return hip_status(dh::launch_splitk_reduce(c->ws, p.splits, m, mem[0].n, mem[0].y, mem[0].ldy, mem[0].epi, s),
+                    "split-K reduce launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dh_last_error(void) { return g_err.c_str(); }
+
+const char* dh_version(void) { return "decide-hip 0.1.0 (gfx950, fp16 MFMA 16x16x32)"; }
+
+int dh_ctx_create(uint32_t flags, dh_ctx** out) {
+  if (!out) return fail(DH_EINVAL, "dh_ctx_create: out is NULL");
+  *out = nullptr;
+  if (flags & ~DH_GEMM_REFERENCE) return fail(DH_EINVAL, "dh_ctx_create: unknown flags 0x%x", flags);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DH_EDEVICE, "dh_ctx_create: no HIP device: %s", hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return fail(DH_EDEVICE, "dh_ctx_create: hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(DH_EDEVICE, "dh_ctx_create: device %d is %s; this library is built for gfx950", dev, prop.gcnArchName);
+  dh_ctx* c = new dh_ctx();
+  c->flags = flags;
+  c->device = dev;
+  *out = c;
+  return ok();
+}
+
+void dh_ctx_destroy(dh_ctx* ctx) {
+  if (!ctx) return;
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  delete ctx;
+}
+
+uint32_t dh_variants_loaded(const dh_ctx* ctx) {
+  return ctx ? (uint32_t)__builtin_popcountll(ctx->used.load(std::memory_order_relaxed)) : 0u;
+}
+
+int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
+               uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
+  int rc = check_gemm(x, ldx, w, ldw, y, ldy, m, n, k, epi);
+  if (rc != DH_OK) return rc;
+  if (!ctx) return fail(DH_EINVAL, "gemm: null context");
+  hipStream_t s = (hipStream_t)stream;
+  if (ctx->flags & DH_GEMM_REFERENCE) {
+    mark(ctx, kKidReference);
+    return hip_status(dh::launch_gemm_reference((const _Float16*)x, ldx, (const _Float16*)w, ldw, y, ldy, m, n, k,
+                                                epi, s),
+                      "gemm reference kernel launch");
+  }
+  const dh::Plan p = choose_plan(ctx, m, n, k, epi);
+  if (p.variant < 0) return fail(DH_EINVAL, "gemm: no plan for M = %u, N = %u, K = %u", m, n, k);
+  dh_gemm_member mem{w, y, ldw, ldy, n, epi};
+  return launch_plan(ctx, s, p, x, ldx, m, k, &mem, 1);
+}
+
+int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, uint32_t m, uint32_t k,
+                       const dh_gemm_member* members, uint32_t count) {
+  if (!members || count < 1 || count > (uint32_t)dh::kMaxMembers)
+    return fail(DH_EINVAL, "gemm grouped: count = %u must be in 1..%d", count, dh::kMaxMembers);
+  uint32_t n_total = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    const dh_gemm_member& mb = members[i];
+    int rc = check_gemm(x, ldx, mb.w, mb.ldw, mb.y, mb.ldy, m, mb.n, k, mb.epi);
+    if (rc != DH_OK) {
+      std::string msg = g_err;
+      return fail(rc, "member %u: %s", i, msg.c_str());
+    }
+    n_total += mb.n;
+  }
+  if (!ctx) return fail(DH_EINVAL, "gemm grouped: null context");
+  hipStream_t s = (hipStream_t)stream;
+  if (ctx->flags & DH_GEMM_REFERENCE) {
+    mark(ctx, kKidReference);
+    for (uint32_t i = 0; i < count; ++i) {
+      const dh_gemm_member& mb = members[i];
+      int rc = hip_status(dh::launch_gemm_reference((const _Float16*)x, ldx, (const _Float16*)mb.w, mb.ldw, mb.y,
+                                                    mb.ldy, m, mb.n, k, mb.epi, s),
+                          "gemm reference kernel launch");
+      if (rc != DH_OK) return rc;
+    }
+    return ok();
+  }
+  dh::Plan p = ctx->forced_variant >= 0 ? dh::plan_make(ctx->forced_variant, 1, m, n_total, k, 0u)
+                                        : dh::plan_grouped(m, n_total, k);
+  if (p.variant < 0) return fail(DH_EINVAL, "gemm grouped: no plan");
+  return launch_plan(ctx, s, p, x, ldx, m, k, members, count);
+}
+
+int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint32_t epi, dh_gemm_plan* out) {
+  if (!out) return fail(DH_EINVAL, "dh_gemm_plan_for: out is NULL");
+  if (epi > 3u || m < 1 || n % 32 || k % 32) return fail(DH_EINVAL, "dh_gemm_plan_for: invalid shape");
+  const dh::Plan p = choose_plan(ctx, m, n, k, epi);
+  if (p.variant < 0) return fail(DH_EINVAL, "dh_gemm_plan_for: no plan");
+  const dh::VariantInfo vi = dh::variant_info(p.variant);
+  out->variant = (uint32_t)p.variant;
+  out->bm = (uint32_t)vi.bm();
+  out->bn = (uint32_t)vi.bn();
+  out->waves = (uint32_t)vi.wn;
+  out->splits = p.splits;
+  out->workgroups = p.grid;
+  out->ws_bytes = p.ws_bytes;
+  return ok();
+}
+
+int dh_gemm_force(dh_ctx* ctx, uint32_t variant, uint32_t splits) {
+  if (!ctx) return fail(DH_EINVAL, "dh_gemm_force: null context");
+  if (variant == UINT32_MAX) {
+    ctx->forced_variant = -1;
+    ctx->forced_splits = 0;
+    return ok();
+  }
+  if (variant >= (uint32_t)dh::variant_count())
+    return fail(DH_EINVAL, "dh_gemm_force: variant %u >= %d", variant, dh::variant_count());
+  if (splits < 1 || splits > 64) return fail(DH_EINVAL, "dh_gemm_force: splits = %u must be in 1..64", splits);
+  ctx->forced_variant = (int)variant;
+  ctx->forced_splits = splits;
+  return ok();
+}
+
+uint32_t dh_gemm_variant_count(void) { return (uint32_t)dh::variant_count(); }
+
+int dh_gemm_variant_info(uint32_t variant, uint32_t* bm, uint32_t* bn, uint32_t* waves, uint32_t* wave_cols) {
+  if (variant >= (uint32_t)dh::variant_count()) return fail(DH_EINVAL, "variant %u out of range", variant);
+  const dh::VariantInfo vi = dh::variant_info((int)variant);
+  if (bm) *bm = (uint32_t)vi.bm();
+  if (bn) *bn = (uint32_t)vi.bn();
+  if (waves) *waves = (uint32_t)vi.wn;
+  if (wave_cols) *wave_cols = (uint32_t)(16 * vi.fn);
+  return ok();
+}
+
+int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
+  if (!ctx) return fail(DH_EINVAL, "dh_warm_up: null context");
+  hipStream_t s = (hipStream_t)stream;
+  // Size the workspace for the largest split-K plan of decide's engine shapes
+  // (gemm_configs.rs:385) at max_m rows.
+  static const uint32_t kShapes[][2] = {{2560, 12352}, {2560, 10240}, {2560, 18432}, {4096, 2560},
+                                        {9216, 2560},  {2560, 2048},  {2560, 8192},  {2560, 6144}};
+  uint64_t need = 0;
+  for (auto& kn : kShapes)
+    for (uint32_t epi = 0; epi < 4; ++epi) {
+      for (uint32_t m = 1; m <= std::max(1u, max_m); m = m < 16 ? m + 1 : m * 2) {
+        const dh::Plan p = choose_plan(ctx, m, kn[1], kn[0], epi);
+        need = std::max(need, p.ws_bytes);
+      }
+      const dh::Plan p = choose_plan(ctx, std::max(1u, max_m), kn[1], kn[0], epi);
+      need = std::max(need, p.ws_bytes);
+    }
+  if (need) {
+    int rc = ensure_ws(ctx, need);
+    if (rc != DH_OK) return rc;
+  }
+  // One tiny launch of every tile variant (M = 16, N = bn, K = 64) into scratch.
+  void* scratch = nullptr;
+  const size_t xb = 16 * 64 * 2, wb = 512 * 64 * 2, yb = 16 * 512 * 4;
+  hipError_t e = hipMalloc(&scratch, xb + wb + yb);
+  if (e != hipSuccess) return fail(DH_ENOMEM, "dh_warm_up: %s", hipGetErrorString(e));
+  e = hipMemsetAsync(scratch, 0, xb + wb + yb, s);
+  int rc = hip_status(e, "dh_warm_up memset");
+  char* base = (char*)scratch;
+  for (int v = 0; v < dh::variant_count() && rc == DH_OK; ++v) {
+    const dh::VariantInfo vi = dh::variant_info(v);
+    dh_gemm_member mem{base + xb, base + xb + wb, 64, (uint32_t)vi.bn(), (uint32_t)vi.bn(), DH_EPI_STORE_F32};
+    rc = launch_plan(ctx, s, dh::plan_make(v, 1, 16, vi.bn(), 64, 0u), base, 64, 16, 64, &mem, 1);
+  }
+  if (rc == DH_OK) {
+    e = hipStreamSynchronize(s);
+    rc = hip_status(e, "dh_warm_up sync");
+  }
+  (void)hipFree(scratch);
+  return rc == DH_OK ? ok() : rc;
+}
+
+int dh_gather_rows_f32(dh_ctx* ctx, void* stream, const float* x, const uint32_t* rowmap, float* out, uint32_t rows,
+                       uint32_t h) {
+  if (!ctx) return fail(DH_EINVAL, "gather_rows_f32: null context");
+  if (rows && (!x || !rowmap || !out)) return fail(DH_EINVAL, "gather_rows_f32: null pointer");
+  mark(ctx, kKidGather32);
+  return hip_status(dh::launch_gather_rows(x, rowmap, out, rows, h, 4, (hipStream_t)stream), "gather_rows_f32");
+}
+
+int dh_gather_rows_f16(dh_ctx* ctx, void* stream, const uint16_t* x, const uint32_t* rowmap, uint16_t* out,
+                       uint32_t rows, uint32_t h) {
+  if (!ctx) return fail(DH_EINVAL, "gather_rows_f16: null context");
+  if (rows && (!x || !rowmap || !out)) return fail(DH_EINVAL, "gather_rows_f16: null pointer");
+  mark(ctx, kKidGather16);
+  return hip_status(dh::launch_gather_rows(x, rowmap, out, rows, h, 2, (hipStream_t)stream), "gather_rows_f16");
+}
+
+int dh_final_head(dh_ctx* ctx, void* stream, const float* x, const float* w, const uint16_t* table,
+                  const uint32_t* cand, const uint32_t* ncand, float* logits, uint32_t rows, uint32_t hidden,
+                  uint32_t max_cand, float eps) {
+  if (hidden == 0 || hidden % 8 != 0 || hidden > 16384)
+    return fail(DH_EINVAL, "final_head: hidden = %u must be a positive multiple of 8, at most 16384", hidden);
+  if (max_cand < 1) return fail(DH_EINVAL, "final_head: max_cand must be at least 1");
+  if (!aligned(table, 16)) return fail(DH_EINVAL, "final_head: table address %p must be a multiple of 16", table);
+  if (!(eps > 0.0f)) return fail(DH_EINVAL, "final_head: eps must be positive");
+  if (!ctx) return fail(DH_EINVAL, "final_head: null context");
+  if (rows && (!x || !w || !table || !cand || !ncand || !logits)) return fail(DH_EINVAL, "final_head: null pointer");
+  mark(ctx, kKidHead);
+  return hip_status(dh::launch_final_head(x, w, table, cand, ncand, logits, rows, hidden, max_cand, eps,
+                                          (hipStream_t)stream),
+                    "final_head");
+}
+
+int dh_rmsnorm_rows(dh_ctx* ctx, void* stream, const float* x, const float* w, uint16_t* y, const uint32_t* rowmap,
+                    uint32_t rows, uint32_t h, uint32_t ld_in, uint32_t ld_out, uint32_t add_one, float eps) {
+  if (h > ld_in || h > ld_out)
+    return fail(DH_EINVAL, "rmsnorm: H = %u exceeds a row stride (ld_in = %u, ld_out = %u)", h, ld_in, ld_out);
+  if (h == 0) return fail(DH_EINVAL, "rmsnorm: H must be at least 1");
+  if (!ctx) return fail(DH_EINVAL, "rmsnorm: null context");
+  if (rows && (!x || !w || !y || !rowmap)) return fail(DH_EINVAL, "rmsnorm: null pointer");
+  mark(ctx, kKidNorm);
+  return hip_status(dh::launch_rmsnorm_rows(x, w, (_Float16*)y, rowmap, rows, h, ld_in, ld_out, add_one != 0, eps,
+                                            (hipStream_t)stream),
+                    "rmsnorm_rows");
+}
+
+int dh_fill_normal_f16(dh_ctx* ctx, void* stream, uint16_t* out, uint64_t n, uint64_t seed, float std) {
+  if (!ctx) return fail(DH_EINVAL, "fill_normal_f16: null context");
+  if (n && !out) return fail(DH_EINVAL, "fill_normal_f16: null pointer");
+  if (!(std >= 0.0f) || !std::isfinite(std)) return fail(DH_EINVAL, "fill_normal_f16: std must be finite and >= 0");
+  mark(ctx, kKidFill);
+  return hip_status(dh::launch_fill_normal_f16(out, n, seed, std, (hipStream_t)stream), "fill_normal_f16");
+}
+
+}  // extern "C"

@@ -1,0 +1,34 @@
+// GEMM launch planner for MI355X: (m, n, k, epi) → tile variant + split-K.
+// decide's counterpart is gemm_configs::plan / recommend
+// (crates/decide-metal/src/gemm_configs.rs:290-314), a table measured on an
+// M1 Pro. This one scores every compiled variant with a bottleneck model of
+// one CDNA4 CU (MFMA issue, LDS bandwidth, L2→CU bandwidth), the wave
+// quantisation of the grid over 256 CUs and the HBM floor, and picks the
+// cheapest. Pure host code: no device needed.
+#pragma once
+
+#include <stdint.h>
+
+namespace dh {
+
+struct Plan {
+  int variant;
+  uint32_t splits;
+  uint32_t kps;       // K per split (multiple of 64)
+  uint32_t mtiles, stripes;
+  uint32_t grid;      // workgroups of the tile kernel
+  uint64_t ws_bytes;  // split-K workspace
+  double est_us;      // model estimate
+};
+
+// Model estimate for one (variant, splits) choice; +inf if the choice is not
+// valid for the shape.
+double plan_estimate_us(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
+// Builds the plan for (variant, splits), filling the derived fields.
+Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
+// Best plan for a single GEMM. `max_ws` caps the split-K workspace bytes.
+Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws);
+// Best variant for a grouped launch of total width n_total (no split-K).
+Plan plan_grouped(uint32_t m, uint32_t n_total, uint32_t k);
+
+}  // namespace dh

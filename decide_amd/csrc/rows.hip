@@ -1,0 +1,173 @@
+// Row kernels around the GEMMs: the bitwise row gathers, the candidate-only
+// LM head, the fp32 → fp16 row RMSNorm that produces every in-projection's
+// activation, and the counter-based N(0, σ) fill used for random-init weights.
+//
+// decide counterparts: kernels/head.metal:8-59 (gather_rows_f32/f16,
+// final_head), kernels/rmsnorm.metal:8-30 (rmsnorm_rows). All are HBM- or
+// latency-bound; one workgroup per row, wave64 shuffles for the reductions.
+#include "dh_kernels.h"
+
+namespace dh {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over a 256-thread workgroup; every thread gets the total. `sh` holds 4 floats.
+__device__ __forceinline__ float block_sum256(float v, float* sh) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) sh[wave] = v;
+  __syncthreads();
+  const float t = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// ---------------------------------------------------------------------------
+// out[i] = x[rowmap[i]], bitwise. One workgroup per output row; 16-byte copies
+// when the row is a whole number of 16-byte vectors, else element copies.
+template <typename T>
+__global__ void gather_rows_kernel(const T* __restrict__ x, const uint32_t* __restrict__ rowmap, T* __restrict__ out,
+                                   uint32_t h) {
+  const uint32_t i = blockIdx.x;
+  const T* src = x + (size_t)rowmap[i] * h;
+  T* dst = out + (size_t)i * h;
+  constexpr uint32_t V = 16 / sizeof(T);
+  const bool vec = (h % V) == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0;
+  if (vec) {
+    for (uint32_t c = threadIdx.x; c < h / V; c += blockDim.x) ((uint4*)dst)[c] = ((const uint4*)src)[c];
+  } else {
+    for (uint32_t c = threadIdx.x; c < h; c += blockDim.x) dst[c] = src[c];
+  }
+}
+
+hipError_t launch_gather_rows(const void* x, const uint32_t* rowmap, void* out, uint32_t rows, uint32_t h,
+                              uint32_t elem_bytes, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  if (elem_bytes == 4)
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3(rows), dim3(256), 0, s, (const uint32_t*)x, rowmap,
+                       (uint32_t*)out, h);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<uint16_t>, dim3(rows), dim3(256), 0, s, (const uint16_t*)x, rowmap,
+                       (uint16_t*)out, h);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Candidate head: one 256-thread workgroup per answer row. The normed row is
+// kept in LDS as fp32; each wave then takes candidates c = wave, wave + 4, …
+// and streams that bf16 table row with 16-byte loads.
+__global__ __launch_bounds__(256) void final_head_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                         const uint16_t* __restrict__ table,
+                                                         const uint32_t* __restrict__ cand,
+                                                         const uint32_t* __restrict__ ncand,
+                                                         float* __restrict__ logits, uint32_t hidden,
+                                                         uint32_t max_cand, float eps) {
+  extern __shared__ float hn[];  // [hidden]
+  __shared__ float sh[4];
+  const uint32_t r = blockIdx.x;
+  const float* xr = x + (size_t)r * hidden;
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < hidden; i += 256) {
+    const float v = xr[i];
+    ss += v * v;
+  }
+  const float inv = rsqrtf(block_sum256(ss, sh) / (float)hidden + eps);
+  for (uint32_t i = threadIdx.x; i < hidden; i += 256) hn[i] = xr[i] * inv * (1.0f + w[i]);
+  __syncthreads();
+  const uint32_t n = min(ncand[r], max_cand);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (uint32_t c = wave; c < n; c += 4) {
+    const uint16_t* er = table + (size_t)cand[(size_t)r * max_cand + c] * hidden;
+    float acc = 0.f;
+    for (uint32_t i = lane * 8; i < hidden; i += 64 * 8) {
+      const uint4 v = *(const uint4*)(er + i);
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc += hn[i + 2 * q] * bf16_to_f32((uint16_t)(wv[q] & 0xffffu));
+        acc += hn[i + 2 * q + 1] * bf16_to_f32((uint16_t)(wv[q] >> 16));
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[(size_t)r * max_cand + c] = acc;
+  }
+}
+
+hipError_t launch_final_head(const float* x, const float* w, const uint16_t* table, const uint32_t* cand,
+                             const uint32_t* ncand, float* logits, uint32_t rows, uint32_t hidden, uint32_t max_cand,
+                             float eps, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(final_head_kernel, dim3(rows), dim3(256), hidden * sizeof(float), s, x, w, table, cand, ncand,
+                     logits, hidden, max_cand, eps);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// y[r] = half(x[rowmap[r]] · rsqrt(mean(x²) + eps) · w'), w' = 1 + w or w.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           _Float16* __restrict__ y,
+                                                           const uint32_t* __restrict__ rowmap, uint32_t h,
+                                                           uint32_t ld_in, uint32_t ld_out, uint32_t add_one,
+                                                           float eps) {
+  __shared__ float sh[4];
+  const float* xr = x + (size_t)rowmap[blockIdx.x] * ld_in;
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < h; i += 256) {
+    const float v = xr[i];
+    ss += v * v;
+  }
+  const float inv = rsqrtf(block_sum256(ss, sh) / (float)h + eps);
+  _Float16* yr = y + (size_t)blockIdx.x * ld_out;
+  for (uint32_t i = threadIdx.x; i < h; i += 256) {
+    const float wv = add_one ? 1.0f + w[i] : w[i];
+    yr[i] = (_Float16)(xr[i] * inv * wv);
+  }
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, _Float16* y, const uint32_t* rowmap, uint32_t rows,
+                               uint32_t h, uint32_t ld_in, uint32_t ld_out, bool add_one, float eps, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, x, w, y, rowmap, h, ld_in, ld_out,
+                     add_one ? 1u : 0u, eps);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// N(0, σ) fill. Element i takes pair p = i / 2: two uniforms in (0, 1) from
+// the splitmix64 finaliser of (seed, 2p) and (seed, 2p + 1), 24-bit mantissas,
+// then Box–Muller (even i: cos branch, odd i: sin branch), rounded to fp16.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_f16_kernel(uint16_t* __restrict__ out, uint64_t n, uint64_t seed, float sd) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t pidx = i >> 1;
+    const uint64_t a = mix64(seed + 0x9e3779b97f4a7c15ull * (2 * pidx + 1));
+    const uint64_t b = mix64(seed + 0x9e3779b97f4a7c15ull * (2 * pidx + 2));
+    const float u1 = ((float)(a >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = ((float)(b >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float rad = sqrtf(-2.0f * logf(u1));
+    const float ang = 6.28318530717958647692f * u2;
+    const float z = (i & 1) ? rad * sinf(ang) : rad * cosf(ang);
+    const _Float16 hv = (_Float16)(z * sd);
+    out[i] = __builtin_bit_cast(uint16_t, hv);
+  }
+}
+
+hipError_t launch_fill_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float sd, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, out, n, seed, sd);
+  return hipGetLastError();
+}
+
+}  // namespace dh

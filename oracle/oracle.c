@@ -1,0 +1,289 @@
+/*
+ * oracle.c — CPU restatement of decide's reference arithmetic for the prefill
+ * GEMM path. TEST INFRASTRUCTURE ONLY: the checker that tests/, the smoke
+ * check and bench.py's cpu_baseline leg compare the HIP library against. The
+ * product (decide_amd/) never links, loads or calls it.
+ *
+ * Each function cites the decide source it restates (paths relative to the
+ * decide tree). Pinning (how each function is checked independently of this
+ * file — see tests/test_oracle.py):
+ *   orc_gemm_nt          KAT + brute force vs numpy float64 matmul (golden fixtures),
+ *                        exact integer closed form, one-hot rows, linearity.
+ *   orc_swiglu_interleaved  decide's KAT swiglu_pairs_blocks (cpu_ref.rs:212-221)
+ *                        plus a closed form on a 64-column row.
+ *   orc_rmsnorm          decide's KAT rmsnorm_by_hand (cpu_ref.rs:204-210) plus
+ *                        scale invariance.
+ *   orc_final_head       composition of rmsnorm and a dot product, checked
+ *                        against numpy float64 on golden fixtures.
+ *   orc_f16_from_f32 / orc_bf16_from_f32 / orc_f16_to_f32
+ *                        numpy float16 (IEEE RNE) on every f16 bit pattern and
+ *                        on a sweep of f32 values; bf16 against a bit-level
+ *                        closed form.
+ *   orc_interleave_gate_up / orc_deinterleave_q_gate
+ *                        hand-written permutation KATs.
+ *   orc_gemm_f32_fast    agrees with orc_gemm_nt within fp32 rounding.
+ * Build: oracle/Makefile (gcc -O2 -fopenmp, no -ffast-math: sums stay in order).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------- fp16 / bf16 rounding (the `half` crate 2.7.1 semantics: IEEE
+ * round-to-nearest-even; testutil.rs:10-12 rounds inputs through them) ---------- */
+
+static uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* binary16 bits → float, exact. */
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t s = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {
+    /* zero or subnormal: m · 2^-24 */
+    const float v = (float)m * (1.0f / 16777216.0f);
+    return s ? -v : v;
+  }
+  if (e == 31) return u2f(s | 0x7f800000u | (m << 13));
+  return u2f(s | ((e + 112u) << 23) | (m << 13));
+}
+
+/* float → binary16 bits, round to nearest even, computed on the value (not
+ * the bit pattern): pick the two neighbouring representable halves and round. */
+uint16_t orc_f16_from_f32(float f) {
+  const uint16_t sign = (f2u(f) >> 16) & 0x8000u;
+  if (isnan(f)) return (uint16_t)(sign | 0x7e00u);
+  double a = fabs((double)f);
+  if (a >= 65520.0) return (uint16_t)(sign | 0x7c00u);
+  /* quantum: 2^-24 below 2^-14, else 2^(floor(log2 a) - 10) */
+  double q;
+  if (a < 6.103515625e-05) {
+    q = 5.9604644775390625e-08;
+  } else {
+    int ex;
+    frexp(a, &ex); /* a = fr · 2^ex, fr in [0.5, 1) */
+    q = ldexp(1.0, ex - 1 - 10);
+  }
+  double n = floor(a / q);
+  const double rem = a - n * q;
+  if (rem > 0.5 * q || (rem == 0.5 * q && fmod(n, 2.0) != 0.0)) n += 1.0;
+  const double v = n * q; /* exact in double */
+  /* encode v */
+  uint16_t bits;
+  if (v < 6.103515625e-05) {
+    bits = (uint16_t)(v / 5.9604644775390625e-08);
+  } else {
+    int ex;
+    const double fr = frexp(v, &ex);                  /* v = fr·2^ex */
+    const uint32_t e16 = (uint32_t)(ex - 1 + 15);      /* biased */
+    const uint32_t m16 = (uint32_t)((fr * 2.0 - 1.0) * 1024.0);
+    bits = (uint16_t)((e16 << 10) | m16);
+  }
+  return (uint16_t)(sign | bits);
+}
+
+float orc_f16_round(float f) { return orc_f16_to_f32(orc_f16_from_f32(f)); }
+
+uint16_t orc_bf16_from_f32(float f) {
+  const uint32_t u = f2u(f);
+  if (isnan(f)) return (uint16_t)((u >> 16) | 0x40u);
+  const uint32_t lsb = (u >> 16) & 1u;
+  return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+float orc_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+void orc_f16_array_to_f32(const uint16_t* h, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32(h[i]);
+}
+void orc_f32_array_to_f16(const float* f, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = orc_f16_from_f32(f[i]);
+}
+
+/* ---------- math helpers (cpu_ref.rs:6-8) ---------- */
+float orc_silu(float x) { return x / (1.0f + expf(-x)); }
+float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* ---------- GEMM (cpu_ref.rs:24-35) ----------
+ * y[i][j] = Σ_k x[i][k]·w[j][k], each product widened to f64 and summed in
+ * k order in f64, stored as f32. Inputs are fp16 bit patterns (exactly the
+ * values the GPU reads), with row strides; y is fp32 [rows, n], row stride ldy.
+ * `rows` (optional) selects which rows of x to compute (row i of y is x row
+ * rows[i]); NULL means rows 0..m-1. Threads split the output rows; every
+ * output is still one in-order f64 sum, so results do not depend on threads. */
+void orc_gemm_nt_f16(const uint16_t* x, uint32_t ldx, const uint16_t* w, uint32_t ldw, float* y, uint32_t ldy,
+                     uint32_t m, uint32_t n, uint32_t k, const uint32_t* rows, int threads) {
+  float* wf = (float*)malloc((size_t)n * k * sizeof(float));
+  for (size_t j = 0; j < n; ++j)
+    for (size_t kk = 0; kk < k; ++kk) wf[j * k + kk] = orc_f16_to_f32(w[j * (size_t)ldw + kk]);
+#ifdef _OPENMP
+  if (threads < 1) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+#endif
+  for (int64_t i = 0; i < (int64_t)m; ++i) {
+    const size_t src = rows ? rows[i] : (size_t)i;
+    float* xf = (float*)malloc((size_t)k * sizeof(float));
+    for (size_t kk = 0; kk < k; ++kk) xf[kk] = orc_f16_to_f32(x[src * ldx + kk]);
+    /* four outputs at a time: four independent in-order sums */
+    size_t j = 0;
+    for (; j + 4 <= n; j += 4) {
+      const float *w0 = wf + j * k, *w1 = w0 + k, *w2 = w1 + k, *w3 = w2 + k;
+      double a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+      for (size_t kk = 0; kk < k; ++kk) {
+        const double xv = xf[kk];
+        a0 += xv * (double)w0[kk];
+        a1 += xv * (double)w1[kk];
+        a2 += xv * (double)w2[kk];
+        a3 += xv * (double)w3[kk];
+      }
+      y[i * (size_t)ldy + j] = (float)a0;
+      y[i * (size_t)ldy + j + 1] = (float)a1;
+      y[i * (size_t)ldy + j + 2] = (float)a2;
+      y[i * (size_t)ldy + j + 3] = (float)a3;
+    }
+    for (; j < n; ++j) {
+      double a = 0;
+      for (size_t kk = 0; kk < k; ++kk) a += (double)xf[kk] * (double)wf[j * k + kk];
+      y[i * (size_t)ldy + j] = (float)a;
+    }
+    free(xf);
+  }
+  free(wf);
+}
+
+/* Same on f32 inputs (cpu_ref::gemm_nt's own signature). */
+void orc_gemm_nt(const float* x, const float* w, float* y, uint32_t m, uint32_t n, uint32_t k) {
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      double a = 0;
+      for (size_t kk = 0; kk < k; ++kk) a += (double)x[i * k + kk] * (double)w[j * k + kk];
+      y[i * n + j] = (float)a;
+    }
+}
+
+/* ---------- SwiGLU over the 16-column interleave (cpu_ref.rs:37-50) ---------- */
+void orc_swiglu_interleaved(const float* y, float* out, uint32_t m, uint32_t n2, uint32_t blk) {
+  const uint32_t n = n2 / 2;
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      const size_t b = j / blk, wv = j % blk;
+      const float g = y[i * n2 + b * 2 * blk + wv];
+      const float u = y[i * n2 + b * 2 * blk + blk + wv];
+      out[i * n + j] = orc_silu(g) * u;
+    }
+}
+
+/* ---------- RMSNorm (cpu_ref.rs:10-22) ---------- */
+void orc_rmsnorm(const float* x, const float* w, float* out, uint32_t rows, uint32_t h, int add_one, float eps) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float* row = x + r * h;
+    double ss = 0;
+    for (size_t i = 0; i < h; ++i) ss += (double)row[i] * (double)row[i];
+    const double ms = ss / (double)h;
+    const float inv = 1.0f / sqrtf((float)ms + eps);
+    for (size_t i = 0; i < h; ++i) {
+      const float wv = add_one ? 1.0f + w[i] : w[i];
+      out[r * h + i] = row[i] * inv * wv;
+    }
+  }
+}
+
+/* ---------- candidate head (cpu_ref.rs:190-198; head.metal:30-59) ----------
+ * logits[r*max_cand + c] = Σ_i norm(x_r)[i] · bf16(table[cand[r*max_cand+c]][i]),
+ * f64 sum, for c < min(ncand[r], max_cand). */
+void orc_final_head(const float* x, const float* w, const uint16_t* table, const uint32_t* cand,
+                    const uint32_t* ncand, float* logits, uint32_t rows, uint32_t hidden, uint32_t max_cand,
+                    float eps) {
+  float* hn = (float*)malloc((size_t)hidden * sizeof(float));
+  for (size_t r = 0; r < rows; ++r) {
+    orc_rmsnorm(x + r * hidden, w, hn, 1, hidden, 1, eps);
+    const uint32_t n = ncand[r] < max_cand ? ncand[r] : max_cand;
+    for (size_t c = 0; c < n; ++c) {
+      const uint16_t* e = table + (size_t)cand[r * max_cand + c] * hidden;
+      double a = 0;
+      for (size_t i = 0; i < hidden; ++i) a += (double)hn[i] * (double)orc_bf16_to_f32(e[i]);
+      logits[r * max_cand + c] = (float)a;
+    }
+  }
+  free(hn);
+}
+
+/* ---------- weight layouts (convert.rs:37-62) ---------- */
+void orc_interleave_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint32_t n, uint32_t k,
+                            uint32_t block) {
+  size_t o = 0;
+  for (size_t b = 0; b < n / block; ++b) {
+    for (size_t r = 0; r < block; ++r, o += k) memcpy(out + o, gate + (b * block + r) * k, k * 2);
+    for (size_t r = 0; r < block; ++r, o += k) memcpy(out + o, up + (b * block + r) * k, k * 2);
+  }
+}
+
+void orc_deinterleave_q_gate(const uint16_t* src, uint16_t* out, uint32_t heads, uint32_t head_dim, uint32_t k) {
+  size_t o = 0;
+  for (size_t part = 0; part < 2; ++part)
+    for (size_t h = 0; h < heads; ++h)
+      for (size_t d = 0; d < head_dim; ++d, o += k) memcpy(out + o, src + ((h * 2 + part) * head_dim + d) * k, k * 2);
+}
+
+/* ---------- fast CPU fp32 GEMM (the timed baseline, not a parity oracle) ----------
+ * y[m][n] = Σ_k x[m][k]·w[n][k] in fp32, blocked, OpenMP over n-blocks. */
+void orc_gemm_f32_fast(const float* x, const float* w, float* y, uint32_t m, uint32_t n, uint32_t k, int threads) {
+#ifdef _OPENMP
+  if (threads < 1) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static)
+#endif
+  for (int64_t jb = 0; jb < (int64_t)n; jb += 8) {
+    const size_t j1 = (size_t)jb + 8 < n ? (size_t)jb + 8 : n;
+    for (size_t i = 0; i < m; ++i) {
+      const float* xr = x + i * k;
+      for (size_t j = (size_t)jb; j < j1; ++j) {
+        const float* wr = w + j * k;
+        float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        size_t kk = 0;
+        for (; kk + 8 <= k; kk += 8)
+          for (int q = 0; q < 8; ++q) a[q] += xr[kk + q] * wr[kk + q];
+        float s = 0;
+        for (int q = 0; q < 8; ++q) s += a[q];
+        for (; kk < k; ++kk) s += xr[kk] * wr[kk];
+        y[i * n + j] = s;
+      }
+    }
+  }
+}
+
+/* ---------- metrics (testutil.rs:14-39 semantics) ---------- */
+/* relative Frobenius error ‖got − want‖ / ‖want‖ in f64 */
+double orc_rel_frobenius(const float* got, const float* want, size_t n) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const double d = (double)got[i] - (double)want[i];
+    num += d * d;
+    den += (double)want[i] * (double)want[i];
+  }
+  return den > 0 ? sqrt(num / den) : sqrt(num);
+}
+
+/* index of the worst violation of |g − w| <= atol + rtol·|w| (NaN fails), or -1 */
+int64_t orc_assert_close(const float* got, const float* want, size_t n, float atol, float rtol) {
+  int64_t worst = -1;
+  float worst_over = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const float err = fabsf(got[i] - want[i]), tol = atol + rtol * fabsf(want[i]);
+    const float over = err - tol;
+    if (!(over <= 0.0f) && (worst < 0 || !(over <= worst_over))) {
+      worst = (int64_t)i;
+      worst_over = over;
+    }
+  }
+  return worst;
+}

@@ -1,0 +1,163 @@
+"""CPU-only checks of the C ABI: the library loads, exports every declared symbol, and rejects
+contract violations before touching a device (decide's Gemm::gemm asserts, gemm.rs:140-163).
+No compute call is made here."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from decide_amd import _lib
+from decide_amd.kernels import Epilogue, plan_for, variants
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    with open(os.path.join(ROOT, "include", "decide_hip.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    # and the binding covers exactly the header
+    assert sorted(_lib.PROTOTYPES) == names
+
+
+def test_version_string():
+    assert b"gfx950" in _lib.load().dh_version()
+
+
+def bad_gemm(**kw):
+    args = dict(x=16, ldx=64, w=16, ldw=64, y=16, ldy=64, m=4, n=64, k=64, epi=0)
+    args.update(kw)
+    lib = _lib.load()
+    rc = lib.dh_gemm_nt(None, None, args["x"], args["ldx"], args["w"], args["ldw"], args["y"], args["ldy"],
+                        args["m"], args["n"], args["k"], args["epi"])
+    return rc, _lib.last_error()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(n=48), "multiples of 32"),
+    (dict(k=40), "multiples of 32"),
+    (dict(m=0), "M must be at least 1"),
+    (dict(ldx=32), "must cover K"),
+    (dict(ldw=32), "must cover K"),
+    (dict(ldy=32), "must cover the 64 output columns"),
+    (dict(ldx=68, k=64), "multiples of 8"),
+    (dict(x=24), "multiples of 16"),
+    (dict(w=8), "multiples of 16"),
+    (dict(ldy=65), "must be even"),
+    (dict(y=4, epi=0), "multiple of 8"),
+    (dict(y=2, epi=3, ldy=32), "multiple of 4"),
+    (dict(epi=4), "epilogue"),
+])
+def test_gemm_contract_violations_are_rejected(kw, msg):
+    rc, err = bad_gemm(**kw)
+    assert rc == _lib.DH_EINVAL
+    assert msg in err, err
+
+
+def test_swiglu_output_width_is_half_n():
+    rc, err = bad_gemm(epi=3, ldy=32)  # n = 64 → 32 output columns: ok contract, then null ctx
+    assert rc == _lib.DH_EINVAL and "null context" in err
+
+
+def test_valid_call_without_context_fails_cleanly():
+    rc, err = bad_gemm()
+    assert rc == _lib.DH_EINVAL and "null context" in err
+
+
+def test_rmsnorm_contract():
+    lib = _lib.load()
+    rc = lib.dh_rmsnorm_rows(None, None, 16, 16, 16, 16, 4, 2600, 2560, 2560, 1, 1e-6)
+    assert rc == _lib.DH_EINVAL and "exceeds a row stride" in _lib.last_error()
+
+
+def test_final_head_contract():
+    lib = _lib.load()
+    rc = lib.dh_final_head(None, None, 16, 16, 16, 16, 16, 16, 3, 2561, 62, 1e-6)
+    assert rc == _lib.DH_EINVAL and "multiple of 8" in _lib.last_error()
+    rc = lib.dh_final_head(None, None, 16, 16, 16, 16, 16, 16, 3, 2560, 0, 1e-6)
+    assert rc == _lib.DH_EINVAL and "max_cand" in _lib.last_error()
+
+
+def test_grouped_member_errors_name_the_member():
+    lib = _lib.load()
+    arr = (_lib.DhGemmMember * 2)()
+    arr[0] = _lib.DhGemmMember(16, 16, 64, 64, 64, 0)
+    arr[1] = _lib.DhGemmMember(16, 16, 64, 64, 48, 0)
+    rc = lib.dh_gemm_nt_grouped(None, None, 16, 64, 4, 64, arr, 2)
+    assert rc == _lib.DH_EINVAL and _lib.last_error().startswith("member 1:")
+    rc = lib.dh_gemm_nt_grouped(None, None, 16, 64, 4, 64, arr, 9)
+    assert rc == _lib.DH_EINVAL and "count" in _lib.last_error()
+
+
+def test_variant_menu_geometry():
+    vs = variants()
+    assert len(vs) >= 8
+    for v in vs:
+        assert v["bm"] % 16 == 0 and v["bn"] % 32 == 0
+        assert v["wave_cols"] % 32 == 0  # SwiGLU pairs 16-column fragments inside a wave
+
+
+@pytest.mark.parametrize("m", [1, 8, 16, 163, 276, 300, 493, 512, 603, 2307])
+@pytest.mark.parametrize("kn", [(2560, 12352), (2560, 10240), (2560, 18432), (4096, 2560), (9216, 2560),
+                                (2560, 2048), (2560, 8192), (2560, 6144), (2560, 9216)])
+def test_planner_covers_engine_shapes(m, kn):
+    """Like decide's plan-covers-every-engine-shape test (gemm_configs.rs:385-400), with this build's M set."""
+    k, n = kn
+    for epi in Epilogue:
+        p = plan_for(m, n, k, epi)
+        v = variants()[p["variant"]]
+        assert p["bm"] == v["bm"] and p["bn"] == v["bn"]
+        assert 1 <= p["splits"] <= 8
+        # the grid covers the output exactly once per split
+        assert p["workgroups"] == -(-m // p["bm"]) * -(-n // p["bn"]) * p["splits"]
+        assert (p["ws_bytes"] == 0) == (p["splits"] == 1)
+        assert p["ws_bytes"] <= 512 << 20
+
+
+def test_layout_functions_match_oracle():
+    import oracle_lib as orc
+
+    lib = _lib.load()
+    rng = np.random.default_rng(1)
+    gate = rng.integers(0, 65536, (64, 40)).astype(np.uint16)
+    up = rng.integers(0, 65536, (64, 40)).astype(np.uint16)
+    out = np.empty((128, 40), dtype=np.uint16)
+    assert lib.dh_interleave_gate_up(gate.ctypes.data, up.ctypes.data, out.ctypes.data, 64, 40, 16) == 0
+    assert np.array_equal(out, orc.interleave_gate_up(gate, up, 16))
+    src = rng.integers(0, 65536, (4 * 2 * 8, 24)).astype(np.uint16)
+    out = np.empty_like(src)
+    assert lib.dh_deinterleave_q_gate(src.ctypes.data, out.ctypes.data, 4, 8, 24) == 0
+    assert np.array_equal(out, orc.deinterleave_q_gate(src, 4, 8))
+    assert lib.dh_interleave_gate_up(gate.ctypes.data, up.ctypes.data, out.ctypes.data, 60, 40, 16) != 0
+
+
+def test_bf16_to_f16_rne_and_overflow_gate():
+    lib = _lib.load()
+    # every bf16 bit pattern that is finite and fits fp16: compare with numpy's IEEE RNE
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f32 = (bits.astype(np.uint32) << 16).view(np.float32)
+    ok = np.isfinite(f32) & (np.abs(f32) < 65504)
+    src = bits[ok]
+    out = np.empty_like(src)
+    counts = (ctypes.c_uint64 * 4)()
+    assert lib.dh_bf16_to_f16(src.ctypes.data, out.ctypes.data, src.size, counts) == 0
+    assert np.array_equal(out, f32[ok].astype(np.float16).view(np.uint16))
+    assert counts[0] == src.size and counts[3] == 0
+    assert counts[2] > 0 and counts[1] > 0  # tiny values flush / become subnormal
+    # an overflowing value aborts (decide's convert refuses it, convert.rs:168-173)
+    big = np.array([0x4780], dtype=np.uint16)  # 65536.0
+    o = np.empty_like(big)
+    assert lib.dh_bf16_to_f16(big.ctypes.data, o.ctypes.data, 1, counts) == _lib.DH_EINVAL
+    assert counts[3] == 1
