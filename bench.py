@@ -99,63 +99,65 @@ def main():
                                    "(multi-GPU sharding is described in DESIGN.md, not implemented)"}))
         sys.exit(2)
 
-    import torch
-
-    from decide_amd import synth
+    from decide_amd import hip, synth
+    from decide_amd.hip import DeviceArray, Event, Stream
     from decide_amd.kernels import Epilogue, Kernels, fill_normal_f16
 
-    if not torch.cuda.is_available():
+    if not hip.available():
         print(json.dumps({"error": "no GPU"}))
         sys.exit(1)
-    dev = torch.device("cuda")
     k = Kernels()
-    stream = torch.cuda.current_stream().cuda_stream
+    st = Stream()
+    stream = st.handle
 
     # ---- resident inputs
-    x = torch.from_numpy(synth.normal_f16(synth.seed_for(21), (M, D), 1.0)).to(dev)
-    x0 = torch.from_numpy(synth.normal_f32(synth.seed_for(24), (M, D), 1.0)).to(dev)
-    wgu = [torch.empty((2 * F, D), dtype=torch.float16, device=dev) for _ in range(WEIGHT_COPIES)]
-    wdn = [torch.empty((D, F), dtype=torch.float16, device=dev) for _ in range(WEIGHT_COPIES)]
+    x = DeviceArray.from_numpy(synth.normal_f16(synth.seed_for(21), (M, D), 1.0))
+    x0 = DeviceArray.from_numpy(synth.normal_f32(synth.seed_for(24), (M, D), 1.0))
+    wgu = [DeviceArray((2 * F, D), np.float16) for _ in range(WEIGHT_COPIES)]
+    wdn = [DeviceArray((D, F), np.float16) for _ in range(WEIGHT_COPIES)]
     for i in range(WEIGHT_COPIES):
-        fill_normal_f16(k.ctx, stream, (wgu[i], 0), wgu[i].numel(), synth.seed_for(22) + 1000 * i, 0.02)
-        fill_normal_f16(k.ctx, stream, (wdn[i], 0), wdn[i].numel(), synth.seed_for(23) + 1000 * i, 0.02)
-    mlp = torch.empty((M, F), dtype=torch.float16, device=dev)
-    res = x0.clone()
+        fill_normal_f16(k.ctx, stream, (wgu[i], 0), 2 * F * D, synth.seed_for(22) + 1000 * i, 0.02)
+        fill_normal_f16(k.ctx, stream, (wdn[i], 0), D * F, synth.seed_for(23) + 1000 * i, 0.02)
+    mlp = DeviceArray((M, F), np.float16)
+    res = DeviceArray((M, D), np.float32)
+    res.copy_(x0)
     k.gemm.warm_up(stream, max_m=M)
+    st.synchronize()
     base_loaded = k.gemm.fast_pipelines()
 
     def step(i, ev=None):
         c = i % WEIGHT_COPIES
         if ev is not None:
-            ev[0].record()
+            ev[0].record(stream)
         k.gemm.gemm(stream, (x, 0), (wgu[c], 0), (mlp, 0), M, 2 * F, D, D, D, F, Epilogue.SwigluF16)
         if ev is not None:
-            ev[1].record()
+            ev[1].record(stream)
         k.gemm.gemm(stream, (mlp, 0), (wdn[c], 0), (res, 0), M, D, F, F, F, D, Epilogue.AddF32)
         if ev is not None:
-            ev[2].record()
+            ev[2].record(stream)
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
+    st.synchronize()
 
-    # ---- timed region: whole steps, and per-kernel event pairs on the same stream
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    # ---- timed region: whole steps, plus per-kernel event pairs on the same stream
+    evs = [[Event() for _ in range(3)] for _ in range(args.steps)]
+    start, stop = Event(), Event()
+    hip.synchronize()
     t0 = time.perf_counter()
-    start.record()
+    start.record(stream)
     for i in range(args.steps):
         step(i, evs[i])
-    stop.record()
-    torch.cuda.synchronize()
+    stop.record(stream)
+    stop.synchronize()
+    hip.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    total_ms = start.elapsed_time(stop)
+    total_ms = start.elapsed_ms(stop)
     ms_per_step = total_ms / args.steps
-    gu_ms = np.array([e[0].elapsed_time(e[1]) for e in evs])
-    dn_ms = np.array([e[1].elapsed_time(e[2]) for e in evs])
+    gu_ms = np.array([e[0].elapsed_ms(e[1]) for e in evs])
+    dn_ms = np.array([e[1].elapsed_ms(e[2]) for e in evs])
     assert k.gemm.fast_pipelines() == base_loaded, "a kernel was loaded inside the timed region"
-    assert torch.isfinite(res).all().item() and torch.isfinite(mlp.float()).all().item()
+    assert np.isfinite(res.numpy()).all() and np.isfinite(mlp.numpy().astype(np.float32)).all()
 
     f_gu, f_dn = flops(M, 2 * F, D), flops(M, D, F)
     value = (f_gu + f_dn) / (ms_per_step * 1e-3) / 1e12

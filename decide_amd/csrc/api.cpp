@@ -313,6 +313,12 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
     dh_gemm_member mem{base + xb, base + xb + wb, 64, (uint32_t)vi.bn(), (uint32_t)vi.bn(), DH_EPI_STORE_F32};
     rc = launch_plan(ctx, s, dh::plan_make(v, 1, 16, vi.bn(), 64, 0u), base, 64, 16, 64, &mem, 1);
   }
+  if (rc == DH_OK && need) {
+    // and the split-K reduction once (two splits of K = 128)
+    const dh::VariantInfo vi = dh::variant_info(0);
+    dh_gemm_member mem{base + xb, base + xb + wb, 128, (uint32_t)vi.bn(), (uint32_t)vi.bn(), DH_EPI_STORE_F32};
+    rc = launch_plan(ctx, s, dh::plan_make(0, 2, 8, vi.bn(), 128, 0u), base, 128, 8, 128, &mem, 1);
+  }
   if (rc == DH_OK) {
     e = hipStreamSynchronize(s);
     rc = hip_status(e, "dh_warm_up sync");

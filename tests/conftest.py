@@ -16,17 +16,17 @@ def pytest_configure(config):
 
 
 @pytest.fixture(scope="session")
-def torch_cuda():
-    """torch with a usable GPU (device memory and streams only)."""
-    import torch
+def gpu():
+    """A usable GPU, reached through the HIP runtime libdecide_hip.so links (no torch)."""
+    from decide_amd import hip
 
-    if not torch.cuda.is_available():
+    if not hip.available():
         pytest.fail("gpu test without a GPU: run with -m 'not gpu' on a CPU host")
-    return torch
+    return hip
 
 
 @pytest.fixture(scope="session")
-def kernels(torch_cuda):
+def kernels(gpu):
     from decide_amd.kernels import Kernels
 
     k = Kernels()
@@ -35,7 +35,7 @@ def kernels(torch_cuda):
 
 
 @pytest.fixture(scope="session")
-def kernels_ref(torch_cuda):
+def kernels_ref(gpu):
     from decide_amd.kernels import GemmImpl, Kernels
 
     k = Kernels(GemmImpl.Baseline)
@@ -44,5 +44,6 @@ def kernels_ref(torch_cuda):
 
 
 @pytest.fixture()
-def stream(torch_cuda):
-    return torch_cuda.cuda.current_stream().cuda_stream
+def stream(gpu):
+    """The legacy default stream (0): synchronous copies order against it."""
+    return 0

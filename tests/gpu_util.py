@@ -5,22 +5,31 @@ from __future__ import annotations
 import numpy as np
 
 import oracle_lib as orc
+from decide_amd.hip import DeviceArray, synchronize
 
 # BASELINE tolerance for one GEMM: relative Frobenius error against the fp32
 # CPU computation of the same inputs.
 GEMM_REL_FROB = 1e-3
 
 
-def to_dev(torch, a: np.ndarray):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+def to_dev(a: np.ndarray) -> DeviceArray:
+    return DeviceArray.from_numpy(np.ascontiguousarray(a))
 
 
-def to_host(t) -> np.ndarray:
-    return t.detach().cpu().numpy()
+def to_host(t: DeviceArray) -> np.ndarray:
+    return t.numpy()
 
 
-def empty(torch, shape, dtype):
-    return torch.empty(shape, dtype=dtype, device="cuda")
+def empty(shape, dtype) -> DeviceArray:
+    return DeviceArray(shape, dtype)
+
+
+def full(shape, dtype, value) -> DeviceArray:
+    return DeviceArray.full(shape, dtype, value)
+
+
+def sync() -> None:
+    synchronize()
 
 
 def sample_rows(m: int, count: int = 48, seed: int = 0) -> np.ndarray:

@@ -1,7 +1,7 @@
 """GPU parity of the GEMM operator (dh_gemm_nt / dh_gemm_nt_grouped) against the oracle.
 
 Everything goes through the C ABI (decide_amd.kernels wraps it with ctypes);
-device memory comes from torch. Oracle: cpu_ref::gemm_nt restated in C
+device memory comes from decide_amd.hip (the same HIP runtime the library links). Oracle: cpu_ref::gemm_nt restated in C
 (f64 sums, fp32 result) on the same fp16 inputs. Bars: relative Frobenius
 error <= 1e-3 per GEMM (BASELINE), bit-exact where the mathematics makes the
 fp32 result exact (integer-valued inputs).
@@ -13,26 +13,26 @@ import pytest
 import oracle_lib as orc
 from decide_amd import synth
 from decide_amd.kernels import Epilogue, variants
-from gpu_util import check_gemm, empty, sample_rows, swiglu_f16, to_dev, to_host
+from gpu_util import check_gemm, empty, full, sample_rows, swiglu_f16, sync, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
 SMALL = [(1, 32, 32), (7, 64, 96), (17, 32, 64), (33, 96, 160), (5, 128, 320), (64, 256, 512), (203, 288, 128)]
 
 
-def run_gemm(torch, kernels, stream, x, w, epi, y0=None, ldy=None):
+def run_gemm(kernels, stream, x, w, epi, y0=None, ldy=None):
     m, k = x.shape
     n = w.shape[0]
     out_cols = n // 2 if epi == Epilogue.SwigluF16 else n
     ldy = ldy or out_cols
-    dt = torch.float32 if epi in (Epilogue.StoreF32, Epilogue.AddF32) else torch.float16
+    dt = np.float32 if epi in (Epilogue.StoreF32, Epilogue.AddF32) else np.float16
     if y0 is not None:
-        y = to_dev(torch, y0)
+        y = to_dev(y0)
     else:
-        y = torch.full((m, ldy), float("nan"), dtype=dt, device="cuda")
-    xd, wd = to_dev(torch, x), to_dev(torch, w)
+        y = full((m, ldy), dt, np.nan)
+    xd, wd = to_dev(x), to_dev(w)
     kernels.gemm.gemm(stream, (xd, 0), (wd, 0), (y, 0), m, n, k, k, k, ldy, epi)
-    torch.cuda.synchronize()
+    sync()
     return to_host(y)[:, :out_cols].astype(np.float32)
 
 
@@ -55,10 +55,10 @@ def inputs(m, n, k, seed):
 
 @pytest.mark.parametrize("m,n,k", SMALL)
 @pytest.mark.parametrize("epi", list(Epilogue))
-def test_small_shapes_planner(torch_cuda, kernels, stream, m, n, k, epi):
+def test_small_shapes_planner(gpu, kernels, stream, m, n, k, epi):
     x, w = inputs(m, n, k, 10 + m)
     y0 = synth.normal_f32(synth.seed_for(99), (m, n), 1.0) if epi == Epilogue.AddF32 else None
-    got = run_gemm(torch_cuda, kernels, stream, x, w, epi, y0)
+    got = run_gemm(kernels, stream, x, w, epi, y0)
     want = oracle_epi(x, w, epi, y0)
     check_gemm(f"m{m} n{n} k{k} {epi.name}", got, want)
     tol = 2e-3 if epi in (Epilogue.StoreF16, Epilogue.SwigluF16) else 1e-4
@@ -66,7 +66,7 @@ def test_small_shapes_planner(torch_cuda, kernels, stream, m, n, k, epi):
 
 
 @pytest.mark.parametrize("variant", range(len(variants())))
-def test_every_variant_and_split_on_integer_inputs_is_exact(torch_cuda, kernels, stream, variant):
+def test_every_variant_and_split_on_integer_inputs_is_exact(gpu, kernels, stream, variant):
     """Integer-valued fp16 in [-4, 4] at K = 288 (4 full stages and a 32-wide tail): every partial
     sum is an integer below 2^24, so any summation order gives the exact fp32 result."""
     rng = np.random.default_rng(variant)
@@ -78,14 +78,14 @@ def test_every_variant_and_split_on_integer_inputs_is_exact(torch_cuda, kernels,
     try:
         for splits in (1, 2, 3):
             kernels.gemm.force(variant, splits)
-            got = run_gemm(torch_cuda, kernels, stream, x, w, Epilogue.StoreF32)
+            got = run_gemm(kernels, stream, x, w, Epilogue.StoreF32)
             assert np.array_equal(got, want), f"variant {variant} splits {splits}"
     finally:
         kernels.gemm.force(None)
 
 
 @pytest.mark.parametrize("variant", range(len(variants())))
-def test_every_variant_swiglu_and_add(torch_cuda, kernels, stream, variant):
+def test_every_variant_swiglu_and_add(gpu, kernels, stream, variant):
     m, k = 37, 192
     n = 2 * variants()[variant]["bn"]
     x, w = inputs(m, n, k, 200 + variant)
@@ -94,37 +94,36 @@ def test_every_variant_swiglu_and_add(torch_cuda, kernels, stream, variant):
         for splits in (1, 2):
             kernels.gemm.force(variant, splits)
             for epi in (Epilogue.SwigluF16, Epilogue.AddF32, Epilogue.StoreF16):
-                got = run_gemm(torch_cuda, kernels, stream, x, w, epi, y0 if epi == Epilogue.AddF32 else None)
+                got = run_gemm(kernels, stream, x, w, epi, y0 if epi == Epilogue.AddF32 else None)
                 check_gemm(f"variant {variant} splits {splits} {epi.name}", got, oracle_epi(x, w, epi, y0))
     finally:
         kernels.gemm.force(None)
 
 
-def test_reference_kernel_matches_oracle(torch_cuda, kernels_ref, stream):
+def test_reference_kernel_matches_oracle(gpu, kernels_ref, stream):
     for (m, n, k) in [(5, 64, 96), (33, 96, 160), (70, 128, 2560)]:
         x, w = inputs(m, n, k, 400 + m)
         for epi in Epilogue:
             y0 = synth.normal_f32(synth.seed_for(401), (m, n), 1.0) if epi == Epilogue.AddF32 else None
-            got = run_gemm(torch_cuda, kernels_ref, stream, x, w, epi, y0)
+            got = run_gemm(kernels_ref, stream, x, w, epi, y0)
             check_gemm(f"reference m{m} {epi.name}", got, oracle_epi(x, w, epi, y0))
 
 
-def test_strides_and_offsets(torch_cuda, kernels, stream):
+def test_strides_and_offsets(gpu, kernels, stream):
     """Row strides wider than K / N and operands addressed at byte offsets inside larger buffers,
     as decide's forward does (e.g. the k|v rows of w_in at ATT_K·HIDDEN·2, forward.rs:1157-1158)."""
-    torch = torch_cuda
     m, n, k = 50, 128, 256
     ldx, ldw, ldy = 320, 264, 160
     rng = np.random.default_rng(11)
     xbig = rng.standard_normal((m + 3, ldx)).astype(np.float16)
     wbig = (rng.standard_normal((n + 64, ldw)) * 0.05).astype(np.float16)
-    xd, wd = to_dev(torch, xbig), to_dev(torch, wbig)
-    y = torch.full((m + 2, ldy), 7.0, dtype=torch.float32, device="cuda")
+    xd, wd = to_dev(xbig), to_dev(wbig)
+    y = full((m + 2, ldy), np.float32, 7.0)
     x_off = 3 * ldx * 2  # start at row 3
     w_off = 64 * ldw * 2  # weight rows 64..
     y_off = 2 * ldy * 4 + 16 * 4  # row 2, column 16
     kernels.gemm.gemm(stream, (xd, x_off), (wd, w_off), (y, y_off), m, n, k, ldx, ldw, ldy, Epilogue.StoreF32)
-    torch.cuda.synchronize()
+    sync()
     yh = to_host(y)
     want = orc.gemm_nt_f16(xbig[3:, :k], wbig[64:, :k])
     check_gemm("strided", yh[2:, 16:16 + n], want)
@@ -133,50 +132,49 @@ def test_strides_and_offsets(torch_cuda, kernels, stream):
     assert (yh[:2] == 7.0).all() and (yh[2:, :16] == 7.0).all()
 
 
-def test_deterministic_and_m_independent_rows(torch_cuda, kernels, stream):
+def test_deterministic_and_m_independent_rows(gpu, kernels, stream):
     x, w = inputs(603, 512, 2560, 500)
-    a = run_gemm(torch_cuda, kernels, stream, x, w, Epilogue.StoreF32)
-    b = run_gemm(torch_cuda, kernels, stream, x, w, Epilogue.StoreF32)
+    a = run_gemm(kernels, stream, x, w, Epilogue.StoreF32)
+    b = run_gemm(kernels, stream, x, w, Epilogue.StoreF32)
     assert np.array_equal(a, b)
     # with the plan pinned, the first rows do not depend on how many rows follow
     p = kernels.gemm.plan(603, 512, 2560, Epilogue.StoreF32)
     try:
         kernels.gemm.force(p["variant"], p["splits"])
-        c = run_gemm(torch_cuda, kernels, stream, x[:17].copy(), w, Epilogue.StoreF32)
+        c = run_gemm(kernels, stream, x[:17].copy(), w, Epilogue.StoreF32)
         assert np.array_equal(c, a[:17])
     finally:
         kernels.gemm.force(None)
 
 
 # ------------------------------------------------------------------ BASELINE configs
-def test_config1_single_gemm_m276(torch_cuda, kernels, stream):
+def test_config1_single_gemm_m276(gpu, kernels, stream):
     """C1: Y = X·Wᵀ, M = 276, K = 2560, N = 9216, fp32 out; checked against the fp32 CPU matmul."""
     m, n, k = 276, 9216, 2560
     x, w = inputs(m, n, k, 1)
-    got = run_gemm(torch_cuda, kernels, stream, x, w, Epilogue.StoreF32)
+    got = run_gemm(kernels, stream, x, w, Epilogue.StoreF32)
     want = orc.gemm_nt_f16(x, w)  # all rows: ~6.5 G MAC, a few seconds on the host
     check_gemm("C1", got, want)
     orc.assert_close("C1", got, want, atol=1e-4, rtol=1e-4)
-    got16 = run_gemm(torch_cuda, kernels, stream, x, w, Epilogue.StoreF16)
+    got16 = run_gemm(kernels, stream, x, w, Epilogue.StoreF16)
     check_gemm("C1 f16", got16, orc.f16_round(want))
 
 
-def test_config2_fused_mlp_m603(torch_cuda, kernels, stream):
+def test_config2_fused_mlp_m603(gpu, kernels, stream):
     """C2: gate|up [603×2560]·[18432×2560]ᵀ with SwiGLU → fp16 [603, 9216]; down [603×9216]·[2560×9216]ᵀ
     added into the fp32 residual. Each GEMM against the oracle on the GPU's own inputs (sampled rows),
     the whole block against the oracle chain."""
-    torch = torch_cuda
     m, d, f = 603, 2560, 9216
     x = synth.normal_f16(synth.seed_for(21), (m, d), 1.0)
     wgu = synth.normal_f16(synth.seed_for(22), (2 * f, d), 0.02)
     wdn = synth.normal_f16(synth.seed_for(23), (d, f), 0.02)
     x0 = synth.normal_f32(synth.seed_for(24), (m, d), 1.0)
-    xd, wgud, wdnd = to_dev(torch, x), to_dev(torch, wgu), to_dev(torch, wdn)
-    mlp = empty(torch, (m, f), torch.float16)
-    res = to_dev(torch, x0)
+    xd, wgud, wdnd = to_dev(x), to_dev(wgu), to_dev(wdn)
+    mlp = empty((m, f), np.float16)
+    res = to_dev(x0)
     kernels.gemm.gemm(stream, (xd, 0), (wgud, 0), (mlp, 0), m, 2 * f, d, d, d, f, Epilogue.SwigluF16)
     kernels.gemm.gemm(stream, (mlp, 0), (wdnd, 0), (res, 0), m, d, f, f, f, d, Epilogue.AddF32)
-    torch.cuda.synchronize()
+    sync()
     mlp_h = to_host(mlp)
     res_h = to_host(res)
     rows = sample_rows(m)
@@ -193,33 +191,32 @@ def test_config2_fused_mlp_m603(torch_cuda, kernels, stream):
     check_gemm("C2 chain (delta)", res_h[rows] - x0[rows], want_chain - x0[rows], rel=2e-3)
 
 
-def rmsnorm_h(torch, kernels, stream, xin, wn):
+def rmsnorm_h(kernels, stream, xin, wn):
     m, d = xin.shape
-    xdv = to_dev(torch, xin)
-    h = empty(torch, (m, d), torch.float16)
-    iota = to_dev(torch, np.arange(m, dtype=np.uint32).view(np.int32))
-    kernels.norm.rmsnorm(stream, (xdv, 0), (to_dev(torch, wn), 0), (h, 0), (iota, 0), m, d, d, d, True)
+    xdv = to_dev(xin)
+    h = empty((m, d), np.float16)
+    iota = to_dev(np.arange(m, dtype=np.uint32).view(np.int32))
+    kernels.norm.rmsnorm(stream, (xdv, 0), (to_dev(wn), 0), (h, 0), (iota, 0), m, d, d, d, True)
     return h
 
 
 @pytest.mark.parametrize("group", ["attention_6144", "attention_10240", "gdn_12352"])
-def test_config3_grouped_projections_m603(torch_cuda, kernels, stream, group):
+def test_config3_grouped_projections_m603(gpu, kernels, stream, group):
     """C3: the projections sharing one RMSNormed activation as ONE grouped launch, then the out
     projection (AddF32). Attention (BASELINE): Q 4096, K 1024, V 1024; attention (decide, gated):
     q|gate 8192, k 1024, v 1024; GDN: qkv 8192, z 4096, b 32, a 32 (decide's column order)."""
-    torch = torch_cuda
     m, d = 603, 2560
     widths = {"attention_6144": [4096, 1024, 1024], "attention_10240": [8192, 1024, 1024],
               "gdn_12352": [8192, 4096, 32, 32]}[group]
     xin = synth.normal_f32(synth.seed_for(31), (m, d), 1.0)
     wn = synth.normal_f32(synth.seed_for(32), (d,), 0.02)
-    h = rmsnorm_h(torch, kernels, stream, xin, wn)
+    h = rmsnorm_h(kernels, stream, xin, wn)
     ws = [synth.normal_f16(synth.seed_for(40 + i), (n, d), 0.02) for i, n in enumerate(widths)]
-    wds = [to_dev(torch, w) for w in ws]
-    ys = [torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda") for n in widths]
+    wds = [to_dev(w) for w in ws]
+    ys = [full((m, n), np.float32, np.nan) for n in widths]
     members = [((wd, 0), d, n, (y, 0), n, Epilogue.StoreF32) for wd, n, y in zip(wds, widths, ys)]
     kernels.gemm.gemm_grouped(stream, (h, 0), d, m, d, members)
-    torch.cuda.synchronize()
+    sync()
     hh = to_host(h)
     rows = sample_rows(m)
     for i, (w, y) in enumerate(zip(ws, ys)):
@@ -231,35 +228,34 @@ def test_config3_grouped_projections_m603(torch_cuda, kernels, stream, group):
     g = synth.normal_f16(synth.seed_for(50), (m, 4096), 1.0)
     wo = synth.normal_f16(synth.seed_for(51), (d, 4096), 0.02)
     x0 = synth.normal_f32(synth.seed_for(52), (m, d), 1.0)
-    res = to_dev(torch, x0)
-    kernels.gemm.gemm(stream, (to_dev(torch, g), 0), (to_dev(torch, wo), 0), (res, 0), m, d, 4096, 4096, 4096,
+    res = to_dev(x0)
+    kernels.gemm.gemm(stream, (to_dev(g), 0), (to_dev(wo), 0), (res, 0), m, d, 4096, 4096, 4096,
                       d, Epilogue.AddF32)
-    torch.cuda.synchronize()
+    sync()
     want = orc.gemm_nt_f16(g, wo, rows=rows)
     check_gemm(f"C3 {group} out", to_host(res)[rows] - x0[rows], want)
 
 
-def test_grouped_equals_fused_single_gemm(torch_cuda, kernels, stream):
+def test_grouped_equals_fused_single_gemm(gpu, kernels, stream):
     """A grouped launch over [W_a; W_b] gives the same bits as one GEMM over the concatenated rows when
     both use the same tile variant (decide fuses by concatenation, convert.rs:204-245)."""
-    torch = torch_cuda
     m, d = 96, 512
     wa = synth.normal_f16(synth.seed_for(60), (256, d), 0.02)
     wb = synth.normal_f16(synth.seed_for(61), (512, d), 0.02)
     x = synth.normal_f16(synth.seed_for(62), (m, d), 1.0)
-    xd = to_dev(torch, x)
-    cat = to_dev(torch, np.concatenate([wa, wb]))
+    xd = to_dev(x)
+    cat = to_dev(np.concatenate([wa, wb]))
     v = kernels.gemm.plan(m, 768, d, Epilogue.StoreF32)["variant"]
     try:
         kernels.gemm.force(v, 1)
-        yf = empty(torch, (m, 768), torch.float32)
+        yf = empty((m, 768), np.float32)
         kernels.gemm.gemm(stream, (xd, 0), (cat, 0), (yf, 0), m, 768, d, d, d, 768, Epilogue.StoreF32)
-        ya, yb = empty(torch, (m, 256), torch.float32), empty(torch, (m, 512), torch.float32)
-        kernels.gemm.gemm_grouped(stream, (xd, 0), d, m, d, [((to_dev(torch, wa), 0), d, 256, (ya, 0), 256,
+        ya, yb = empty((m, 256), np.float32), empty((m, 512), np.float32)
+        kernels.gemm.gemm_grouped(stream, (xd, 0), d, m, d, [((to_dev(wa), 0), d, 256, (ya, 0), 256,
                                                               Epilogue.StoreF32),
-                                                             ((to_dev(torch, wb), 0), d, 512, (yb, 0), 512,
+                                                             ((to_dev(wb), 0), d, 512, (yb, 0), 512,
                                                               Epilogue.StoreF32)])
-        torch.cuda.synchronize()
+        sync()
     finally:
         kernels.gemm.force(None)
     f = to_host(yf)
@@ -268,15 +264,14 @@ def test_grouped_equals_fused_single_gemm(torch_cuda, kernels, stream):
 
 
 @pytest.mark.parametrize("kn", [(2560, 12352), (2560, 10240), (2560, 18432), (4096, 2560), (9216, 2560)])
-def test_config4_projections_m2307(torch_cuda, kernels, stream, kn):
+def test_config4_projections_m2307(gpu, kernels, stream, kn):
     """C4: every projection GEMM of one hybrid layer at M = 2,307 (sampled rows against the oracle)."""
-    torch = torch_cuda
     k, n = kn
     m = 2307
     x, w = inputs(m, n, k, 70 + n)
     epi = Epilogue.SwigluF16 if n == 18432 else (Epilogue.AddF32 if n == 2560 else Epilogue.StoreF32)
     y0 = synth.normal_f32(synth.seed_for(71), (m, n), 1.0) if epi == Epilogue.AddF32 else None
-    got = run_gemm(torch, kernels, stream, x, w, epi, y0)
+    got = run_gemm(kernels, stream, x, w, epi, y0)
     rows = sample_rows(m, 40, seed=n)
     y = orc.gemm_nt_f16(x, w, rows=rows)
     if epi == Epilogue.SwigluF16:
