@@ -1,33 +1,45 @@
 // MFMA tile GEMM for gfx950: Y = epi(X · Wᵀ), X fp16 [M, K], W fp16 [N, K]
 // (both K-contiguous, decide's NT layout), fp32 accumulation.
 //
-// Role in decide: the `gemm_nt_fast*` tile kernels and, with FM = 1, the
+// Role in decide: the `gemm_nt_fast*` tile kernels and, with FM <= 2, the
 // small-M weight-streaming kernel `gemm_nt_small`
 // (kernels/gemm_fast.metal:240-351, 429-566). The design is MI355X's own:
 //
-//   * Workgroup = WN wavefronts (64 lanes) side by side along N. Every wave
-//     computes all BM = 16·FM rows of the tile for its own 16·FN columns with
-//     v_mfma_f32_16x16x32_f16, so the X tile is the only operand the waves
-//     share: it is staged through LDS, double-buffered (one barrier per stage).
-//   * W is used by exactly one wave per workgroup, so it never touches LDS:
-//     each lane loads its MFMA B operands straight from global memory into
-//     VGPRs, PD stages (of 64 K) ahead of use, 16-byte loads, every 128-byte
-//     row segment read whole by four lanes. This is the weight-streaming form;
-//     at skinny M it is what keeps HBM busy.
+//   * Workgroup = 4 wavefronts side by side along N, 64 columns each, every
+//     wave computing all BM = 16·FM rows of the tile with
+//     v_mfma_f32_16x16x32_f16 (BN = 256).
+//   * Both operands reach LDS by coalesced DMA (global_load_lds_dwordx4:
+//     eight lanes per 128-byte row segment, no VGPR staging). The MFMA B
+//     operand wants 16 different W rows per load instruction; gathered
+//     straight from L2 that pattern runs at well under half the bandwidth of
+//     the coalesced DMA, so W goes through LDS too.
+//   * LDS rows are 128 bytes (one 64-wide K stage), unpadded; the 16-byte
+//     chunk c of row rr is stored at chunk c ^ ((rr >> 1) & 7): every DMA
+//     instruction writes 1 KB contiguously and the ds_read_b128 of 16
+//     consecutive rows spreads over all banks.
+//   * Rings of NBX X-tile and NBW W-tile stage buffers (W, the operand that
+//     streams from HBM, gets the deeper one). The DMAs the next stage needs
+//     are issued at the start of a stage, the rest are spread over its MFMAs;
+//     one vmcnt wait and one barrier end each stage.
+//   * The hot loop (LDS reads two fragments ahead, MFMAs, waits, DMAs) is
+//     inline asm in program order: accumulators pinned in AGPRs so the
+//     register allocator cannot rotate them, and exact wait counts.
 //   * K order inside a stage: sub-step s (0, 1) covers k0 + 32s .. +32, and
-//     lane group g = lane / 16 supplies k0 + 32s + 8g .. +8 for both operands,
-//     so A and B always pair the same k.
+//     lane group g = lane / 16 supplies k0 + 32s + 8g .. +8 for both operands.
 //   * M tail in-kernel: rows past M re-read row M-1 (never stored). N tail:
-//     columns past N re-read row N-1 of W (never stored).
+//     columns past N re-read row N-1 of W (never stored). K % 64 == 32: one
+//     unpipelined 32-wide sub-stage at the end.
 //   * Workgroup ids are renumbered so that the consecutive work items of one
 //     XCD (the hardware deals workgroups round-robin over the 8 XCDs) walk the
 //     M tiles of one W column stripe back to back: the stripe is fetched from
 //     HBM once and re-read from that XCD's L2.
-//   * Epilogues (decide's four, gemm.rs:15-26) straight from the accumulator
-//     registers; SwiGLU pairs fragment j (gate) with j + 1 (up), the
-//     16-column blocks of the gate|up interleave.
+//   * Epilogues (decide's four, gemm.rs:15-26) through LDS so every wave
+//     writes whole output rows with 16-byte stores; SwiGLU pairs fragment j
+//     (gate) with j + 1 (up), the 16-column blocks of the gate|up interleave.
 //   * Split-K: workgroups of split s write fp32 partials; a second kernel sums
 //     them in split order (deterministic) and applies the epilogue.
+#include <type_traits>
+
 #include "dh_kernels.h"
 
 namespace dh {
@@ -36,7 +48,18 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& fn) {
+  if constexpr (B < E) {
+    fn(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(fn);
+  }
+}
+
+// silu(v) = v / (1 + e^-v) with the hardware exp and reciprocal (about 1 ulp
+// each); decide's kernels use fast-math exp for silu as well (common.h:5-7).
+__device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // Workgroup b runs on XCD b % 8. Renumber so XCD x owns one contiguous range
 // of work ids (a bijection on [0, G)).
@@ -46,21 +69,344 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t G) {
   return xcd * per + (xcd < rem ? xcd : rem) + local;
 }
 
-template <int FM, int FN, int WN, int PD>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * WN, 64 * WN), amdgpu_waves_per_eu(1, 1)))
-void gemm_tile_kernel(const TileArgs p) {
-  constexpr int BM = 16 * FM, BN = 16 * FN * WN, NT = 64 * WN;
-  constexpr int LDA = kBK + 8;  // LDS row stride in halves (16-byte pad)
-  // The X tile is copied by every thread alike: XPT 16-byte chunks each, so
-  // the LDS tile has XR >= BM rows (rows past BM are loaded, never read).
-  constexpr int RPP = NT / (kBK / 8);  // rows one pass of the workgroup copies
-  constexpr int XR = (BM + RPP - 1) / RPP * RPP;
-  constexpr int XPT = XR / RPP;
-  constexpr int TILE = XR * LDA;  // halves per LDS buffer
-  static_assert(FN % 2 == 0, "SwiGLU pairs fragments j, j+1: FN must be even");
-  __shared__ __attribute__((aligned(16))) _Float16 lds[2 * TILE];
+// Epilogue through LDS for the 4-wave, 256-column tiles: the accumulators of
+// CR = 64 rows at a time are written to LDS in row-major fp32 (row stride
+// BN + 4 floats: the four lane groups of a store land 16 banks apart), then
+// read back so that each wave writes whole output rows with 16-byte stores.
+// `stage` must hold 64 · 260 floats and be free (all main-loop LDS reads done).
+template <int FM, int FN>
+__device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split,
+                                               uint32_t m0, uint32_t n0, int wave, int r, int g, float* stage) {
+  constexpr int BN = 16 * FN * 4, LDR = BN + 4, CR = 64, BM = 16 * FM;
+  const uint32_t M = p.m, N = p.mem[mi].n;
+  const int tid = threadIdx.x;
+  const uint32_t epi = p.mem[mi].epi, ldy = p.mem[mi].ldy;
+  char* Y = (char*)p.mem[mi].y;
+  const bool partial = p.splits > 1;
+  const uint32_t esz = (partial || epi == 0u || epi == 2u) ? 4u : 2u;
+  const bool vec16 = partial || ((((uintptr_t)Y) % 16) == 0 && ((size_t)ldy * esz) % 16 == 0);
+  if (epi == 3u && !partial) {
+    // SwiGLU in registers, then the fp16 tile [BM][BN/2] through LDS (row
+    // stride BN + 16 bytes) and out with 16-byte stores, 16 lanes per row.
+    constexpr int OW = BN / 2;          // output halves per tile row
+    constexpr int LDH = OW + 8;         // LDS row stride in halves
+    _Float16* st = (_Float16*)stage;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; j += 2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          st[(i * 16 + 4 * g + e) * LDH + wave * 8 * FN + (j / 2) * 16 + r] =
+              (_Float16)(silu_f(acc[i][j][e]) * acc[i][j + 1][e]);
+    __syncthreads();
+    constexpr int OQ = OW / 8;  // 16-byte chunks per row
+#pragma unroll
+    for (int it = 0; it < (BM * OQ + 255) / 256; ++it) {
+      const int item = it * 256 + tid;
+      if (item >= BM * OQ) break;
+      const int row = item / OQ, oq = item % OQ;
+      const uint32_t grow = m0 + row;
+      if (grow >= M || n0 + 32 * (oq / 2) >= N) continue;
+      const h8 o = *(const h8*)(st + row * LDH + oq * 8);
+      _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + oq * 8;
+      if (vec16) {
+        *(h8*)dst = o;
+      } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int q = 0; q < 8; q += 2) *(h2*)(dst + q) = h2{o[q], o[q + 1]};
+      }
+    }
+    return;
+  }
+  static_for<0, (BM + CR - 1) / CR>([&](auto cc) {
+    constexpr int c0 = decltype(cc)::value * CR;
+    constexpr int i0 = c0 / 16, i1 = (c0 + CR) / 16 < FM ? (c0 + CR) / 16 : FM;
+    constexpr int rows = (BM - c0) < CR ? (BM - c0) : CR;
+    if (m0 + c0 >= M) return;
+    __syncthreads();
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          stage[(i * 16 - c0 + 4 * g + e) * LDR + wave * 16 * FN + j * 16 + r] = acc[i][j][e];
+    __syncthreads();
+    if (epi == 3u && !partial) {
+      // 8 fp16 outputs per item: output chunk oq of the tile row (16 per row)
+      constexpr int OQ = BN / 16;  // output chunks of 8 halves per row
+#pragma unroll
+      for (int it = 0; it < (rows * OQ + 255) / 256; ++it) {
+        const int item = it * 256 + tid;
+        if (item >= rows * OQ) break;
+        const int row = item / OQ, oq = item % OQ;
+        const uint32_t grow = m0 + c0 + row;
+        const uint32_t gcol = n0 + 32 * (oq / 2) + (oq % 2) * 8;  // first gate column
+        if (grow >= M || gcol >= N) continue;
+        const float* gp = stage + row * LDR + 32 * (oq / 2) + (oq % 2) * 8;
+        const f4 ga = *(const f4*)gp, gb = *(const f4*)(gp + 4);
+        const f4 ua = *(const f4*)(gp + 16), ub = *(const f4*)(gp + 20);
+        h8 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          o[q] = (_Float16)(silu_f(ga[q]) * ua[q]);
+          o[q + 4] = (_Float16)(silu_f(gb[q]) * ub[q]);
+        }
+        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + oq * 8;
+        if (vec16) {
+          *(h8*)dst = o;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; q += 2) {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            *(h2*)(dst + q) = h2{o[q], o[q + 1]};
+          }
+        }
+      }
+      return;
+    }
+    // one float4 of a tile row per item; a wave covers one whole 256-column row
+#pragma unroll
+    for (int it = 0; it < (rows * (BN / 4) + 255) / 256; ++it) {
+      const int item = it * 256 + tid;
+      if (item >= rows * (BN / 4)) break;
+      const int row = item / (BN / 4), cq = item % (BN / 4);
+      const uint32_t grow = m0 + c0 + row, gcol = n0 + 4 * cq;
+      if (grow >= M || gcol >= N) continue;
+      const f4 v = *(const f4*)(stage + row * LDR + 4 * cq);
+      if (partial) {
+        *(f4*)(p.ws + ((size_t)split * M + grow) * N + gcol) = v;
+      } else if (epi == 1u) {
+        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + gcol;
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        *(h2*)dst = h2{(_Float16)v[0], (_Float16)v[1]};
+        *(h2*)(dst + 2) = h2{(_Float16)v[2], (_Float16)v[3]};
+      } else {
+        float* dst = (float*)Y + (size_t)grow * ldy + gcol;
+        typedef float fl2 __attribute__((ext_vector_type(2)));
+        if (vec16) {
+          f4 o = v;
+          if (epi == 2u) o += *(const f4*)dst;
+          *(f4*)dst = o;
+        } else {
+          fl2 lo = fl2{v[0], v[1]}, hi = fl2{v[2], v[3]};
+          if (epi == 2u) {
+            lo += *(const fl2*)dst;
+            hi += *(const fl2*)(dst + 2);
+          }
+          *(fl2*)dst = lo;
+          *(fl2*)(dst + 2) = hi;
+        }
+      }
+    }
+  });
+}
 
-  // ---- work item of this workgroup
+// ---------------------------------------------------------------------------
+// Hot-loop building blocks, written as inline asm so they issue exactly in
+// program order and the accumulators stay pinned in AGPRs.
+// LDS 16-byte read at LDS byte address base + OFF (OFF < 65536).
+template <int OFF>
+__device__ __forceinline__ void ds_read16(h8& dst, uint32_t base) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(OFF));
+}
+
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// MFMA as volatile asm: stays in program order with the reads and waits.
+__device__ __forceinline__ void mfma_acc_v(f4& acc, const h8& a, const h8& b) {
+  asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void tie(h8& v) { asm volatile("" : "+v"(v)); }
+
+// 16-byte-per-lane DMA global → LDS: lane l's 16 bytes at sbase + voff land at
+// LDS byte address m0 + 16·l. M0 is written in the same statement; one wait
+// state separates the write from its use.
+// M0 is a reserved register to the compiler, which warns that it may not be
+// preserved across the statement; nothing else in these kernels reads M0
+// (the build checks the generated code for other M0 uses).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(uint32_t m0, uint32_t voff, const void* sbase) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(m0), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// ---------------------------------------------------------------------------
+// The tile pipeline: NBX X-tile and NBW W-tile stage buffers; stage kt issues
+// X(kt + NBX - 1) and W(kt + NBW - 1). The DMAs a stage issues are ordered so
+// that the ones needed by the next stage come first; one vmcnt wait then
+// covers exactly those.
+template <int FM, int NBX, int NBW>
+struct Pipe {
+  static constexpr int FN = 4, NT = 256, LAX = NBX - 1, LAW = NBW - 1;
+  static constexpr int U = (NBX == NBW) ? NBX : NBX * NBW;  // unroll (lcm for 2, 3)
+  static constexpr int LAM = LAX > LAW ? LAX : LAW;
+  static constexpr int BM = 16 * FM;
+  static constexpr int XR = (BM + 31) / 32 * 32;
+  static constexpr int XPW = XR / 32;
+  static constexpr int WPW = 16 * FN / 8;
+  static constexpr int XBYTES = XR * 128, WBYTES = 256 * 128;
+  static constexpr int WRING = NBX * XBYTES;  // offset of the W ring
+  static constexpr int LDS_BYTES = NBX * XBYTES + NBW * WBYTES;
+  // outstanding DMAs allowed at the end of a stage (those not needed next)
+  static constexpr int KEEP = (LAX >= 2 ? XPW : 0) + (LAW >= 2 ? WPW : 0);
+  static_assert(NBX >= 2 && NBW >= 2 && NBX <= 3 && NBW <= 3, "ring depths 2 or 3");
+
+  f4 acc[FM][FN];
+  uint32_t xoff[XPW];
+  uint32_t woff[WPW];
+  uint32_t a0, a1;
+  uint32_t lds_addr;
+  uint32_t xm0[XPW];
+  uint32_t wm0;
+  uint32_t wrow;
+  const char* wbase;
+  const char* xbase;
+
+  template <int B>
+  __device__ __forceinline__ void dma_x(int kt) {
+    const char* xb = xbase + (size_t)kt * (kBK * 2);
+#pragma unroll
+    for (int q = 0; q < XPW; ++q) dma16(lds_addr + B * XBYTES + xm0[q], xoff[q], xb);
+  }
+  template <int B>
+  __device__ __forceinline__ void dma_w(int kt) {
+    const char* wb = wbase + (size_t)kt * (kBK * 2);
+#pragma unroll
+    for (int q = 0; q < WPW; ++q) dma16(lds_addr + WRING + B * WBYTES + wm0 + q * 1024, woff[q], wb);
+  }
+  // issue the DMAs of stage kt for the rings (X slot BX, W slot BW), needed-next first
+  template <int BX, int BW>
+  __device__ __forceinline__ void issue(int kt, int nst) {
+    const bool ix = kt + LAX < nst, iw = kt + LAW < nst;
+    if (LAX <= LAW) {
+      if (ix) dma_x<(BX + LAX) % NBX>(kt + LAX);
+      if (iw) dma_w<(BW + LAW) % NBW>(kt + LAW);
+    } else {
+      if (iw) dma_w<(BW + LAW) % NBW>(kt + LAW);
+      if (ix) dma_x<(BX + LAX) % NBX>(kt + LAX);
+    }
+  }
+  template <int F>
+  static constexpr int a_imm() {
+    return (F % FM) * 16 * 128;
+  }
+  // One stage's DMA number D (compile time): X blocks first, then W blocks,
+  // into ring slots NX / NW, for stages kx / kw.
+  template <int D, int NX, int NW>
+  __device__ __forceinline__ void dma_one(int kx, int kw) {
+    if constexpr (D < XPW) {
+      dma16(lds_addr + NX * XBYTES + xm0[D], xoff[D], xbase + (size_t)kx * (kBK * 2));
+    } else {
+      dma16(lds_addr + WRING + NW * WBYTES + wm0 + (D - XPW) * 1024, woff[D - XPW],
+            wbase + (size_t)kw * (kBK * 2));
+    }
+  }
+  // The MFMAs of a stage from ring slots (BX, BW). With IL, the DMAs of stage
+  // kt + LAX / kt + LAW are spread over the fragments (one every NF / DPW),
+  // so the address unit sees a steady stream instead of a burst that would
+  // stall the issuing waves.
+  template <int BX, int BW, bool IL, bool XFIRST>
+  __device__ __forceinline__ void compute(int kt) {
+    constexpr int NF = 2 * FM, AD = 2, DPW = XPW + WPW;
+    constexpr int NXS = (BX + LAX) % NBX, NWS = (BW + LAW) % NBW;
+    const uint32_t xb = lds_addr + BX * XBYTES;
+    const uint32_t b0 = xb + a0, b1 = xb + a1;
+    const uint32_t wb = lds_addr + WRING + BW * WBYTES + wrow;
+    const uint32_t w0 = wb + a0, w1 = wb + a1;
+    h8 wf[FN][2];
+    static_for<0, FN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      ds_read16<j * 16 * 128>(wf[j][0], w0);
+      ds_read16<j * 16 * 128>(wf[j][1], w1);
+    });
+    h8 a[AD + 1];
+    static_for<0, AD>([&](auto fc) {
+      constexpr int f = decltype(fc)::value;
+      ds_read16<a_imm<f>()>(a[f], f / FM ? b1 : b0);
+    });
+    static_for<0, NF>([&](auto fc) {
+      constexpr int f = decltype(fc)::value;
+      if constexpr (IL) {
+        // The DMAs the next stage needs (the operand with lookahead 1) go out
+        // together before the first fragment; the others (lookahead 2) are
+        // spread one every NF / n fragments over the rest of the stage.
+        constexpr int NEED = (LAX == 1 ? XPW : 0) + (LAW == 1 ? WPW : 0);
+        constexpr int REST = DPW - NEED;
+        static_for<0, DPW>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          constexpr int dd = XFIRST ? d : (d < WPW ? d + XPW : d - WPW);  // issue order
+          constexpr int at = d < NEED ? 0 : (REST > 0 ? (d - NEED) * NF / REST : 0);
+          if constexpr (at == f) dma_one<dd, NXS, NWS>(kt + LAX, kt + LAW);
+        });
+      }
+      if constexpr (f + AD < NF) ds_read16<a_imm<f + AD>()>(a[(f + AD) % (AD + 1)], (f + AD) / FM ? b1 : b0);
+      constexpr int later = (NF - 1 - f) < AD ? (NF - 1 - f) : AD;
+      wait_lgkm<later>();
+      tie(a[f % (AD + 1)]);
+      if constexpr (f == 0) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          tie(wf[j][0]);
+          tie(wf[j][1]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) mfma_acc_v(acc[f % FM][j], a[f % (AD + 1)], wf[j][f / FM]);
+    });
+  }
+  // Stage kt; U-periodic slot indices are compile-time via Q = kt mod U.
+  template <int Q>
+  __device__ __forceinline__ void stage(int kt, int nst, bool steady) {
+    constexpr int BX = Q % NBX, BW = Q % NBW;
+    if (steady) {
+      compute<BX, BW, true, (LAX <= LAW)>(kt);
+    } else {
+      issue<BX, BW>(kt, nst);
+      compute<BX, BW, false, true>(kt);
+    }
+    if (kt + 1 < nst) {
+      // DMAs still allowed in flight: this stage's issues not needed by stage kt + 1
+      if (steady) {
+        wait_vm<KEEP>();
+      } else {
+        const bool ix2 = LAX >= 2 && kt + LAX < nst, iw2 = LAW >= 2 && kt + LAW < nst;
+        if (ix2 && iw2)
+          wait_vm<XPW + WPW>();
+        else if (ix2)
+          wait_vm<XPW>();
+        else if (iw2)
+          wait_vm<WPW>();
+        else
+          wait_vm<0>();
+      }
+    }
+    __syncthreads();
+  }
+};
+
+template <int FM, int NBX, int NBW>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_tile_kernel(const TileArgs p) {
+  using P = Pipe<FM, NBX, NBW>;
+  constexpr int FN = P::FN, BN = 16 * FN * 4;
+  constexpr int LDSB = P::LDS_BYTES > 64 * (BN + 4) * 4 ? P::LDS_BYTES : 64 * (BN + 4) * 4;
+  __shared__ __attribute__((aligned(1024))) char lds[LDSB];
+
   const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t mt = wid % p.mtiles;
   const uint32_t q = wid / p.mtiles;
@@ -70,203 +416,144 @@ void gemm_tile_kernel(const TileArgs p) {
 #pragma unroll
   for (int i = 1; i < kMaxMembers; ++i)
     if (i < (int)p.count && gs >= p.mem[i].stripe_begin) mi = i;
-  const _Float16* __restrict__ W = p.mem[mi].w;
-  const uint32_t ldw = p.mem[mi].ldw, N = p.mem[mi].n;
-  const uint32_t M = p.m;
-  const uint32_t m0 = mt * BM;
+  const uint32_t ldw = p.mem[mi].ldw, N = p.mem[mi].n, M = p.m;
+  const uint32_t m0 = mt * P::BM;
   const uint32_t n0 = (gs - p.mem[mi].stripe_begin) * BN;
   const uint32_t kb = split * p.kps;
   const uint32_t ke = min(p.k, kb + p.kps);
-  const int nst = (int)((ke - kb) / kBK);  // full 64-wide stages
-  const bool half_tail = ((ke - kb) % kBK) != 0;  // one more 32-wide sub-stage
+  const int nst = (int)((ke - kb) / kBK);
+  const bool half_tail = ((ke - kb) % kBK) != 0;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-
-  // ---- X (A operand) chunk addresses of this thread: rows xrow0 + c·RPP,
-  // 16-byte column xcol of the 128-byte stage row.
-  const int xrow0 = tid / (kBK / 8), xcol = tid % (kBK / 8);
-  const _Float16* xp[XPT];
+  P pp;
+  pp.lds_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  pp.wbase = (const char*)(p.mem[mi].w + kb);
+  pp.xbase = (const char*)(p.x + kb);
+  const uint32_t sw = (uint32_t)((r >> 1) & 7);
+  pp.a0 = r * 128 + ((g ^ sw) * 16);
+  pp.a1 = r * 128 + (((4 + g) ^ sw) * 16);
 #pragma unroll
-  for (int c = 0; c < XPT; ++c) {
-    const uint32_t grow = min(m0 + (uint32_t)(xrow0 + c * RPP), M - 1);
-    xp[c] = p.x + (size_t)grow * p.ldx + kb + xcol * 8;
+  for (int c = 0; c < P::XPW; ++c) {
+    const int G = 4 * c + wave;
+    const uint32_t row = 8 * G + (lane >> 3);
+    const uint32_t chunk = (uint32_t)((lane & 7) ^ ((4 * G + (lane >> 4)) & 7));
+    pp.xoff[c] = (min(m0 + row, M - 1) * p.ldx + chunk * 8) * 2;
+    pp.xm0[c] = (uint32_t)G * 1024;
   }
-  const int xl0 = xrow0 * LDA + xcol * 8;  // LDS offset of chunk 0; chunk c adds c·RPP·LDA
-  // ---- W (B operand) row addresses of this lane: fragment j covers columns
-  // n0 + wave·16·FN + 16 j .. + 16; this lane feeds column (… + r).
-  const _Float16* wp[FN];
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const uint32_t n = min(n0 + (uint32_t)(wave * 16 * FN + j * 16 + r), N - 1);
-    wp[j] = W + (size_t)n * ldw + kb + g * 8;
+  for (int c = 0; c < P::WPW; ++c) {
+    const int G = 8 * wave + c;
+    const uint32_t row = 8 * G + (lane >> 3);
+    const uint32_t chunk = (uint32_t)((lane & 7) ^ ((4 * G + (lane >> 4)) & 7));
+    pp.woff[c] = (min(n0 + row, N - 1) * ldw + chunk * 8) * 2;
   }
-
-  f4 acc[FM][FN];
+  pp.wm0 = (uint32_t)wave * 8 * 1024;
+  pp.wrow = (uint32_t)wave * 64 * 128;
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) pp.acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  h8 wr[PD][FN][2];
-  u4 xr[XPT];
-
-  auto load_w = [&](h8 (&dst)[FN][2], int kt) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) dst[j][s] = *(const h8*)(wp[j] + kt * kBK + s * 32);
-  };
-  auto load_x = [&](int kt) {
-#pragma unroll
-    for (int c = 0; c < XPT; ++c) xr[c] = *(const u4*)(xp[c] + kt * kBK);
-  };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < XPT; ++c) *(u4*)(lds + buf * TILE + xl0 + c * RPP * LDA) = xr[c];
-  };
-
-  // ---- prologue
-#pragma unroll
-  for (int pp = 0; pp < PD; ++pp)
-    if (pp < nst) load_w(wr[pp], pp);
   if (nst > 0) {
-    load_x(0);
-    store_x(0);
-  }
-  __syncthreads();
-
-  // ---- one pipeline stage: X(kt + 1) global → registers, the 2·FM·FN MFMAs
-  // of stage kt, W(kt + PD) → the ring slot just consumed, X(kt + 1) → LDS.
-  auto stage = [&](int kt, h8 (&wbuf)[FN][2], bool prefetch, bool more) {
-    if (more) load_x(kt + 1);
-    // Keep the X loads ahead of the MFMAs: they have one stage to land.
-    __builtin_amdgcn_sched_barrier(0);
-    const _Float16* A = lds + (kt & 1) * TILE;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const h8 a = *(const h8*)(A + (i * 16 + r) * LDA + s * 32 + g * 8);
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, wbuf[j][s], acc[i][j], 0, 0, 0);
+    // prologue: X(0..LAX-1) and W(0..LAW-1) in flight; stage 0's land first.
+    pp.template dma_x<0>(0);
+    pp.template dma_w<0>(0);
+    int later = 0;  // DMAs issued after stage 0's
+    if (nst > 1) {
+      if (P::LAX >= 2) {
+        pp.template dma_x<1 % NBX>(1);
+        later += P::XPW;
+      }
+      if (P::LAW >= 2) {
+        pp.template dma_w<1 % NBW>(1);
+        later += P::WPW;
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    if (prefetch) load_w(wbuf, kt + PD);
-    if (more) store_x((kt + 1) & 1);
+    if (later == P::XPW + P::WPW)
+      wait_vm<P::XPW + P::WPW>();
+    else if (later == P::XPW)
+      wait_vm<P::XPW>();
+    else if (later == P::WPW)
+      wait_vm<P::WPW>();
+    else
+      wait_vm<0>();
     __syncthreads();
-  };
 
-  // ---- steady state: groups of PD stages that all prefetch, with no
-  // conditions inside, so the compiler's load counters stay exact.
-  int kt = 0;
-  for (; kt + 2 * PD <= nst; kt += PD) {
-#pragma unroll
-    for (int pp = 0; pp < PD; ++pp) stage(kt + pp, wr[pp], true, true);
-  }
-  // ---- drain: the last < 2·PD stages (kt is a multiple of PD here)
-#pragma unroll
-  for (int pp = 0; pp < 2 * PD; ++pp) {
-    if (kt + pp < nst) stage(kt + pp, wr[pp % PD], kt + pp + PD < nst, kt + pp + 1 < nst);
-  }
-
-  // ---- K % 64 == 32: one last 32-wide sub-stage, not pipelined
-  if (half_tail) {
-    const int kt = nst;
-    h8 wt[FN];
-#pragma unroll
-    for (int j = 0; j < FN; ++j) wt[j] = *(const h8*)(wp[j] + kt * kBK);
-    if (xcol < 4) {  // the first 32 halves of each row only
-#pragma unroll
-      for (int c = 0; c < XPT; ++c) *(u4*)(lds + xl0 + c * RPP * LDA) = *(const u4*)(xp[c] + kt * kBK);
+    int kt = 0;
+    for (; kt + P::U - 1 + P::LAM < nst; kt += P::U) {
+      static_for<0, P::U>([&](auto qc) {
+        constexpr int qq = decltype(qc)::value;
+        pp.template stage<qq>(kt + qq, nst, true);
+      });
     }
+    static_for<0, P::U + P::LAM>([&](auto qc) {
+      constexpr int qq = decltype(qc)::value;
+      if (kt + qq < nst) pp.template stage<qq % P::U>(kt + qq, nst, false);
+    });
+  }
+
+  if (half_tail) {  // K % 64 == 32: one 32-wide sub-stage into slot 0, unpipelined
+    const char* xb = pp.xbase + (size_t)nst * (kBK * 2);
+    const char* wb = pp.wbase + (size_t)nst * (kBK * 2);
+#pragma unroll
+    for (int c = 0; c < P::XPW; ++c) {
+      const int G = 4 * c + wave;
+      const uint32_t chunk = (uint32_t)((lane & 7) ^ ((4 * G + (lane >> 4)) & 7));
+      if (chunk < 4) dma16(pp.lds_addr + pp.xm0[c], pp.xoff[c], xb);
+    }
+#pragma unroll
+    for (int c = 0; c < P::WPW; ++c) {
+      const int G = 8 * wave + c;
+      const uint32_t chunk = (uint32_t)((lane & 7) ^ ((4 * G + (lane >> 4)) & 7));
+      if (chunk < 4) dma16(pp.lds_addr + P::WRING + pp.wm0 + c * 1024, pp.woff[c], wb);
+    }
+    wait_vm<0>();
     __syncthreads();
+    const uint32_t b0 = pp.lds_addr + pp.a0;
+    const uint32_t w0 = pp.lds_addr + P::WRING + pp.wrow + pp.a0;
+    h8 wf[FN];
+    static_for<0, FN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      ds_read16<j * 16 * 128>(wf[j], w0);
+    });
+    static_for<0, FM>([&](auto fc) {
+      constexpr int i = decltype(fc)::value;
+      h8 a;
+      ds_read16<i * 16 * 128>(a, b0);
+      wait_lgkm<0>();
+      tie(a);
+      if constexpr (i == 0) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const h8 a = *(const h8*)(lds + (i * 16 + r) * LDA + g * 8);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, wt[j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-  // ---- epilogue. Accumulator element e of fragment (i, j) in lane (r, g) is
-  // row m0 + 16 i + 4 g + e, column nw + 16 j + r.
-  const uint32_t nw = n0 + wave * 16 * FN;
-  if (p.splits > 1) {
-    float* ws = p.ws + (size_t)split * M * N;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t row = m0 + i * 16 + g * 4 + e;
-        if (row >= M) continue;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const uint32_t col = nw + j * 16 + r;
-          if (col < N) ws[(size_t)row * N + col] = acc[i][j][e];
-        }
+        for (int j = 0; j < FN; ++j) tie(wf[j]);
       }
-    return;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) mfma_acc_v(pp.acc[i][j], a, wf[j]);
+    });
   }
-  const uint32_t epi = p.mem[mi].epi, ldy = p.mem[mi].ldy;
-  void* Y = p.mem[mi].y;
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t row = m0 + i * 16 + g * 4 + e;
-      if (row >= M) continue;
-      const size_t rb = (size_t)row * ldy;
-      if (epi == 3u) {
-#pragma unroll
-        for (int j = 0; j < FN; j += 2) {
-          const uint32_t col = nw + j * 16 + r;
-          if (col >= N) continue;
-          const float o = silu_f(acc[i][j][e]) * acc[i][j + 1][e];
-          ((_Float16*)Y)[rb + (nw + j * 16) / 2 + r] = (_Float16)o;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const uint32_t col = nw + j * 16 + r;
-          if (col >= N) continue;
-          const float v = acc[i][j][e];
-          if (epi == 0u)
-            ((float*)Y)[rb + col] = v;
-          else if (epi == 1u)
-            ((_Float16*)Y)[rb + col] = (_Float16)v;
-          else
-            ((float*)Y)[rb + col] += v;
-        }
-      }
-    }
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  store_tile_lds<FM, FN>(pp.acc, p, mi, split, m0, n0, wave, r, g, (float*)lds);
 }
 
-// ---- the compiled menu. (FM, FN, WN, PD)
+// ---- the compiled menu: (FM, NBX, NBW). BM = 16·FM rows, BN = 256.
 #define DH_TILE_MENU(X) \
-  X(1, 2, 4, 4)         \
-  X(2, 2, 4, 4)         \
-  X(4, 2, 4, 3)         \
-  X(4, 4, 4, 3)         \
-  X(6, 4, 4, 2)         \
-  X(8, 4, 4, 2)         \
-  X(10, 4, 4, 2)        \
-  X(12, 4, 4, 2)        \
-  X(13, 4, 4, 2)        \
-  X(14, 4, 4, 2)        \
-  X(15, 4, 4, 2)        \
-  X(16, 4, 4, 2)        \
-  X(8, 2, 4, 2)         \
-  X(13, 2, 4, 2)
+  X(1, 3, 3)            \
+  X(2, 3, 3)            \
+  X(4, 3, 3)            \
+  X(6, 3, 3)            \
+  X(8, 3, 3)            \
+  X(10, 3, 3)           \
+  X(12, 2, 3)           \
+  X(13, 2, 3)           \
+  X(14, 2, 3)
 
 struct VariantEntry {
   VariantInfo info;
   void (*fn)(const TileArgs);
 };
 
-#define DH_TILE_ENTRY(FM, FN, WN, PD) {{FM, FN, WN}, gemm_tile_kernel<FM, FN, WN, PD>},
+#define DH_TILE_ENTRY(FM, NBX, NBW) {{FM, 4, 4}, gemm_tile_kernel<FM, NBX, NBW>},
 static const VariantEntry kVariants[] = {DH_TILE_MENU(DH_TILE_ENTRY)};
 #undef DH_TILE_ENTRY
 
@@ -280,43 +567,55 @@ hipError_t launch_tile(int v, const TileArgs& a, uint32_t grid, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K reduction: y = epi(Σ_s ws[s]) summed in split order. One thread per
-// output element (SwiGLU: per fp16 output, reading its gate and up sums).
+// Split-K reduction: y = epi(Σ_s ws[s]) summed in split order (deterministic).
+// One thread per 4 consecutive outputs: 16-byte partial reads.
 __global__ void splitk_reduce_kernel(const float* __restrict__ ws, uint32_t splits, uint32_t m, uint32_t n, void* y,
                                      uint32_t ldy, uint32_t epi) {
   const uint32_t ncols = epi == 3u ? n / 2 : n;
-  const size_t total = (size_t)m * ncols;
+  const size_t total = (size_t)m * (ncols / 4);
   const size_t plane = (size_t)m * n;
   for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
-    const uint32_t row = (uint32_t)(t / ncols), oc = (uint32_t)(t % ncols);
+    const uint32_t row = (uint32_t)(t / (ncols / 4)), oc = (uint32_t)(t % (ncols / 4)) * 4;
+    f4 v;
     if (epi == 3u) {
       const uint32_t gc = (oc / kSwigluBlock) * 2 * kSwigluBlock + oc % kSwigluBlock;
       const float* pg = ws + (size_t)row * n + gc;
-      float gsum = 0.f, usum = 0.f;
-      for (uint32_t s = 0; s < splits; ++s) {
-        gsum += pg[s * plane];
-        usum += pg[s * plane + kSwigluBlock];
+      f4 gs = *(const f4*)pg, us = *(const f4*)(pg + kSwigluBlock);
+      for (uint32_t s = 1; s < splits; ++s) {
+        gs += *(const f4*)(pg + s * plane);
+        us += *(const f4*)(pg + s * plane + kSwigluBlock);
       }
-      ((_Float16*)y)[(size_t)row * ldy + oc] = (_Float16)(silu_f(gsum) * usum);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = silu_f(gs[q]) * us[q];
     } else {
       const float* pp = ws + (size_t)row * n + oc;
-      float v = 0.f;
-      for (uint32_t s = 0; s < splits; ++s) v += pp[s * plane];
-      const size_t o = (size_t)row * ldy + oc;
-      if (epi == 0u)
-        ((float*)y)[o] = v;
-      else if (epi == 1u)
-        ((_Float16*)y)[o] = (_Float16)v;
-      else
-        ((float*)y)[o] += v;
+      v = *(const f4*)pp;
+      for (uint32_t s = 1; s < splits; ++s) v += *(const f4*)(pp + s * plane);
+    }
+    const size_t o = (size_t)row * ldy + oc;
+    typedef float fl2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    if (epi == 0u || epi == 2u) {
+      float* dst = (float*)y + o;  // 8-byte aligned (contract): two float2 accesses
+      fl2 lo = fl2{v[0], v[1]}, hi = fl2{v[2], v[3]};
+      if (epi == 2u) {
+        lo += *(const fl2*)dst;
+        hi += *(const fl2*)(dst + 2);
+      }
+      *(fl2*)dst = lo;
+      *(fl2*)(dst + 2) = hi;
+    } else {
+      _Float16* dst = (_Float16*)y + o;  // 4-byte aligned (contract)
+      *(h2*)dst = h2{(_Float16)v[0], (_Float16)v[1]};
+      *(h2*)(dst + 2) = h2{(_Float16)v[2], (_Float16)v[3]};
     }
   }
 }
 
 hipError_t launch_splitk_reduce(const float* ws, uint32_t splits, uint32_t m, uint32_t n, void* y, uint32_t ldy,
                                 uint32_t epi, hipStream_t s) {
-  const size_t total = (size_t)m * (epi == 3u ? n / 2 : n);
-  const uint32_t blocks = (uint32_t)std::min<size_t>((total + 255) / 256, 8192);
+  const size_t total = (size_t)m * ((epi == 3u ? n / 2 : n) / 4);
+  const uint32_t blocks = (uint32_t)std::min<size_t>((total + 255) / 256, 16384);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, ws, splits, m, n, y, ldy, epi);
   return hipGetLastError();
 }

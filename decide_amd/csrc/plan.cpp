@@ -1,11 +1,21 @@
-// See plan.h. The model constants are MI355X's public figures: 256 CUs of
-// 4 SIMDs at 2.4 GHz, one v_mfma_f32_16x16x32_f16 per 16 clocks per SIMD
-// (2.5 PFLOP/s dense fp16), 128 B/clk of LDS and 64 B/clk of L2→CU bandwidth
-// per CU, 8 TB/s of HBM.
+// See plan.h. Two parts:
+//   * a table measured on an MI355X (decide_amd/tune_gemm.py): for decide's
+//     engine shapes (K, N) at M in {1, 3, 8, 16, 24, 48, 96, 163, 276, 490,
+//     603, 1024, 2307}, the fastest (tile variant, split-K) with weights
+//     streaming from HBM — the MI355X counterpart of decide's M1 Pro
+//     RECOMMENDED table (crates/decide-metal/src/gemm_configs.rs:247-283);
+//   * a cost model for every other shape, calibrated on the same
+//     measurements: a 64-wide K stage of a BM = 16·FM tile takes about
+//     0.115·FM µs (MFMA issue plus the DMA and barrier it waits on), blocks
+//     run in rounds of 256 (one per CU), the weights stream at most at
+//     6 TB/s, and split-K adds a reduction pass over S + 2 fp32 planes.
+// The table entry is used when the requested M is within 12 % of a measured
+// M for that (K, N); otherwise the model picks the variant and split.
 #include "plan.h"
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <limits>
 
 #include "dh_kernels.h"
@@ -13,28 +23,153 @@
 namespace dh {
 
 namespace {
-constexpr double kClockHz = 2.4e9;
 constexpr double kCUs = 256.0;
-constexpr double kHbmBps = 8.0e12;
-constexpr double kLdsBpc = 128.0;   // LDS bytes per clock per CU
-constexpr double kL2Bpc = 64.0;     // L2 → CU bytes per clock per CU
-constexpr double kStageOverhead = 1.15;
-constexpr double kLaunchUs = 2.0;   // fixed cost of one kernel launch
-constexpr double kBlockUs = 0.6;    // workgroup start-up and epilogue
+constexpr double kHbmBps = 6.0e12;      // sustained HBM read bandwidth (measured streaming copy)
+constexpr double kStageUsPerFM = 0.115;  // µs per 64-wide stage per 16-row fragment
+constexpr double kMinStageUs = 0.35;     // a stage is never cheaper than its DMA round trip
+constexpr double kLaunchUs = 3.0;        // kernel launch + prologue + epilogue
 constexpr uint32_t kSplitMenu[] = {1, 2, 3, 4, 6, 8};
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+struct Measured {
+  uint32_t k, n, m;
+  int variant;
+  uint32_t splits;
+};
+
+// {k, n, m, variant, splits}: fastest on an MI355X (gfx950, 256 CUs), the
+// variant index into the compiled menu (gemm_tile.hip: FM 1, 2, 4, 6, 8, 10,
+// 12, 13, 14), weights rotated over > 256 MB.
+const Measured kMeasured[] = {
+    {2560, 12352, 1, 0, 4},  // 15.75 us
+    {2560, 12352, 3, 0, 4},  // 15.89 us
+    {2560, 12352, 8, 0, 4},  // 16.12 us
+    {2560, 12352, 16, 0, 4},  // 16.67 us
+    {2560, 12352, 24, 1, 4},  // 17.5 us
+    {2560, 12352, 48, 2, 4},  // 20.42 us
+    {2560, 12352, 96, 3, 4},  // 25.36 us
+    {2560, 12352, 163, 3, 2},  // 31.1 us
+    {2560, 12352, 276, 2, 1},  // 36.29 us
+    {2560, 12352, 490, 4, 1},  // 46.9 us
+    {2560, 12352, 603, 4, 1},  // 47.69 us
+    {2560, 12352, 1024, 7, 1},  // 68.45 us
+    {2560, 12352, 2307, 5, 1},  // 153.91 us
+    {2560, 10240, 1, 0, 6},  // 14.32 us
+    {2560, 10240, 3, 0, 6},  // 14.47 us
+    {2560, 10240, 8, 0, 6},  // 14.91 us
+    {2560, 10240, 16, 0, 4},  // 15.51 us
+    {2560, 10240, 24, 1, 6},  // 16.28 us
+    {2560, 10240, 48, 1, 3},  // 19.11 us
+    {2560, 10240, 96, 2, 3},  // 22.51 us
+    {2560, 10240, 163, 2, 2},  // 27.04 us
+    {2560, 10240, 276, 3, 2},  // 32.97 us
+    {2560, 10240, 490, 3, 1},  // 39.63 us
+    {2560, 10240, 603, 4, 1},  // 45.73 us
+    {2560, 10240, 1024, 6, 1},  // 62.2 us
+    {2560, 10240, 2307, 7, 1},  // 131.87 us
+    {2560, 18432, 1, 0, 3},  // 20.96 us
+    {2560, 18432, 3, 0, 3},  // 21.16 us
+    {2560, 18432, 8, 0, 3},  // 21.36 us
+    {2560, 18432, 16, 0, 3},  // 22.01 us
+    {2560, 18432, 24, 1, 3},  // 23.04 us
+    {2560, 18432, 48, 2, 3},  // 26.11 us
+    {2560, 18432, 96, 3, 3},  // 31.9 us
+    {2560, 18432, 163, 2, 1},  // 36.77 us
+    {2560, 18432, 276, 3, 1},  // 41.4 us
+    {2560, 18432, 490, 6, 1},  // 55.3 us
+    {2560, 18432, 603, 7, 1},  // 59.71 us
+    {2560, 18432, 1024, 5, 1},  // 91.92 us
+    {2560, 18432, 2307, 6, 1},  // 212.48 us
+    {4096, 2560, 1, 0, 8},  // 9.97 us
+    {4096, 2560, 3, 1, 8},  // 10.68 us
+    {4096, 2560, 8, 0, 6},  // 10.82 us
+    {4096, 2560, 16, 0, 8},  // 11.03 us
+    {4096, 2560, 24, 0, 8},  // 11.29 us
+    {4096, 2560, 48, 0, 8},  // 12.41 us
+    {4096, 2560, 96, 1, 6},  // 14.07 us
+    {4096, 2560, 163, 1, 4},  // 16.97 us
+    {4096, 2560, 276, 2, 4},  // 20.02 us
+    {4096, 2560, 490, 3, 4},  // 26.0 us
+    {4096, 2560, 603, 3, 3},  // 29.27 us
+    {4096, 2560, 1024, 4, 3},  // 38.92 us
+    {4096, 2560, 2307, 3, 1},  // 58.86 us
+    {9216, 2560, 1, 1, 8},  // 18.2 us
+    {9216, 2560, 3, 0, 8},  // 18.26 us
+    {9216, 2560, 8, 1, 8},  // 18.82 us
+    {9216, 2560, 16, 0, 8},  // 19.08 us
+    {9216, 2560, 24, 0, 8},  // 19.38 us
+    {9216, 2560, 48, 0, 8},  // 19.32 us
+    {9216, 2560, 96, 1, 8},  // 21.14 us
+    {9216, 2560, 163, 2, 8},  // 25.17 us
+    {9216, 2560, 276, 3, 6},  // 32.51 us
+    {9216, 2560, 490, 3, 4},  // 39.94 us
+    {9216, 2560, 603, 4, 4},  // 46.76 us
+    {9216, 2560, 1024, 4, 3},  // 60.68 us
+    {9216, 2560, 2307, 3, 1},  // 115.69 us
+    {2560, 2048, 1, 0, 8},  // 8.85 us
+    {2560, 2048, 3, 0, 6},  // 9.06 us
+    {2560, 2048, 8, 0, 8},  // 9.49 us
+    {2560, 2048, 16, 0, 6},  // 9.86 us
+    {2560, 2048, 24, 0, 6},  // 9.95 us
+    {2560, 2048, 48, 0, 4},  // 10.46 us
+    {2560, 2048, 96, 0, 4},  // 11.31 us
+    {2560, 2048, 163, 1, 3},  // 13.45 us
+    {2560, 2048, 276, 1, 3},  // 15.84 us
+    {2560, 2048, 490, 1, 2},  // 17.32 us
+    {2560, 2048, 603, 2, 3},  // 18.97 us
+    {2560, 2048, 1024, 1, 1},  // 22.46 us
+    {2560, 2048, 2307, 3, 1},  // 33.61 us
+    {2560, 8192, 1, 0, 6},  // 12.96 us
+    {2560, 8192, 3, 0, 6},  // 13.29 us
+    {2560, 8192, 8, 0, 6},  // 13.47 us
+    {2560, 8192, 16, 0, 6},  // 13.85 us
+    {2560, 8192, 24, 0, 4},  // 14.38 us
+    {2560, 8192, 48, 1, 4},  // 16.08 us
+    {2560, 8192, 96, 2, 4},  // 19.82 us
+    {2560, 8192, 163, 2, 2},  // 25.24 us
+    {2560, 8192, 276, 3, 2},  // 31.19 us
+    {2560, 8192, 490, 2, 1},  // 35.83 us
+    {2560, 8192, 603, 3, 1},  // 39.29 us
+    {2560, 8192, 1024, 4, 1},  // 47.95 us
+    {2560, 8192, 2307, 5, 1},  // 103.4 us
+    {2560, 6144, 1, 0, 8},  // 11.93 us
+    {2560, 6144, 3, 0, 8},  // 12.06 us
+    {2560, 6144, 8, 0, 8},  // 12.54 us
+    {2560, 6144, 16, 0, 8},  // 12.91 us
+    {2560, 6144, 24, 1, 6},  // 13.61 us
+    {2560, 6144, 48, 1, 4},  // 14.96 us
+    {2560, 6144, 96, 2, 4},  // 17.97 us
+    {2560, 6144, 163, 2, 3},  // 21.33 us
+    {2560, 6144, 276, 2, 2},  // 26.01 us
+    {2560, 6144, 490, 2, 1},  // 34.15 us
+    {2560, 6144, 603, 2, 1},  // 34.72 us
+    {2560, 6144, 1024, 4, 1},  // 45.2 us
+    {2560, 6144, 2307, 4, 1},  // 87.98 us
+    {2560, 9216, 1, 0, 6},  // 13.47 us
+    {2560, 9216, 3, 0, 6},  // 13.52 us
+    {2560, 9216, 8, 0, 6},  // 14.03 us
+    {2560, 9216, 16, 0, 6},  // 14.5 us
+    {2560, 9216, 24, 1, 6},  // 15.18 us
+    {2560, 9216, 48, 2, 6},  // 18.18 us
+    {2560, 9216, 96, 2, 3},  // 21.59 us
+    {2560, 9216, 163, 2, 2},  // 26.09 us
+    {2560, 9216, 276, 3, 2},  // 31.59 us
+    {2560, 9216, 490, 3, 1},  // 38.56 us
+    {2560, 9216, 603, 3, 1},  // 40.06 us
+    {2560, 9216, 1024, 5, 1},  // 52.69 us
+    {2560, 9216, 2307, 6, 1},  // 122.78 us
+};
 }  // namespace
 
 Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
   const VariantInfo v = variant_info(variant);
   Plan p{};
   p.variant = variant;
-  p.splits = splits;
   const uint32_t stages = ceil_div(k, kBK);
+  splits = std::max(1u, std::min(splits, stages));
   p.kps = ceil_div(stages, splits) * kBK;
-  // Splits that would be empty are dropped.
-  p.splits = ceil_div(k, p.kps);
+  p.splits = ceil_div(k, p.kps);  // splits that would be empty are dropped
   p.mtiles = ceil_div(m, (uint32_t)v.bm());
   p.stripes = ceil_div(n, (uint32_t)v.bn());
   p.grid = p.mtiles * p.stripes * p.splits;
@@ -45,36 +180,25 @@ Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k,
 
 double plan_estimate_us(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
   const VariantInfo v = variant_info(variant);
-  if (epi == 3u && (v.fn % 2) != 0) return std::numeric_limits<double>::infinity();
   const uint32_t stages = ceil_div(k, kBK);
-  if (splits > stages) return std::numeric_limits<double>::infinity();
+  if (splits < 1 || splits > stages) return std::numeric_limits<double>::infinity();
   const uint32_t st_per_split = ceil_div(stages, splits);
   splits = ceil_div(stages, st_per_split);
   const double mtiles = ceil_div(m, (uint32_t)v.bm()), stripes = ceil_div(n, (uint32_t)v.bn());
   const double blocks = mtiles * stripes * splits;
-  // Per-stage clocks of one workgroup (one wave per SIMD).
-  const double mfma_clk = 32.0 * v.fm * v.fn;
-  const double lds_clk = (1.0 + v.wn) * 16.0 * v.fm * 128.0 / kLdsBpc;
-  const double l2_clk = (v.wn * v.fn * 2048.0 + 16.0 * v.fm * 128.0) / kL2Bpc;
-  const double stage_clk = std::max(mfma_clk, std::max(lds_clk, l2_clk)) * kStageOverhead;
-  const double block_us = st_per_split * stage_clk / kClockHz * 1e6 + kBlockUs;
   const double rounds = std::ceil(blocks / kCUs);
-  const double compute_us = rounds * block_us;
-  // HBM floor: W once, X once, the output (read too for AddF32), split-K partials twice.
+  const double stage_us = std::max(kMinStageUs, kStageUsPerFM * v.fm);
+  const double compute_us = rounds * st_per_split * stage_us;
   const double out_b = (epi == 0u || epi == 2u) ? 4.0 : 2.0;
   const double out_cols = epi == 3u ? n / 2.0 : n;
-  double bytes = 2.0 * n * k + 2.0 * m * k + out_b * m * out_cols * (epi == 2u ? 2.0 : 1.0);
-  double extra_us = 0.0;
-  if (splits > 1) {
-    const double part = 4.0 * splits * (double)m * n;
-    bytes += part;
-    extra_us = kLaunchUs + (part + out_b * m * out_cols) / kHbmBps * 1e6;
-  }
-  const double hbm_us = bytes / kHbmBps * 1e6;
-  return std::max(compute_us, hbm_us) + kLaunchUs + extra_us;
+  const double hbm_us = (2.0 * n * k + 2.0 * m * k + out_b * m * out_cols) / kHbmBps * 1e6;
+  double t = std::max(compute_us, hbm_us) + kLaunchUs;
+  if (splits > 1) t += kLaunchUs + (splits + 2.0) * m * n * 4.0 / kHbmBps * 1e6;
+  return t;
 }
 
-Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws) {
+namespace {
+Plan plan_model(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws) {
   Plan best{};
   best.est_us = std::numeric_limits<double>::infinity();
   best.variant = -1;
@@ -89,16 +213,29 @@ Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws
   }
   return best;
 }
+}  // namespace
+
+Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws) {
+  const Measured* near = nullptr;
+  double best_rel = 0.12;
+  for (const Measured& e : kMeasured) {
+    if (e.k != k || e.n != n || e.variant >= variant_count()) continue;
+    const double rel = std::fabs((double)m - e.m) / e.m;
+    if (rel <= best_rel) {
+      best_rel = rel;
+      near = &e;
+    }
+  }
+  if (near) {
+    const Plan p = plan_make(near->variant, near->splits, m, n, k, epi);
+    if (p.ws_bytes <= max_ws) return p;
+  }
+  return plan_model(m, n, k, epi, max_ws);
+}
 
 Plan plan_grouped(uint32_t m, uint32_t n_total, uint32_t k) {
-  Plan best{};
-  best.est_us = std::numeric_limits<double>::infinity();
-  best.variant = -1;
-  for (int v = 0; v < variant_count(); ++v) {
-    const double t = plan_estimate_us(v, 1, m, n_total, k, 0u);
-    if (t < best.est_us) best = plan_make(v, 1, m, n_total, k, 0u);
-  }
-  return best;
+  // Members share X and launch together; plan as one GEMM of the summed width.
+  return plan_gemm(m, n_total, k, 0u, 0);
 }
 
 }  // namespace dh

@@ -1,10 +1,10 @@
 // GEMM launch planner for MI355X: (m, n, k, epi) → tile variant + split-K.
 // decide's counterpart is gemm_configs::plan / recommend
 // (crates/decide-metal/src/gemm_configs.rs:290-314), a table measured on an
-// M1 Pro. This one scores every compiled variant with a bottleneck model of
-// one CDNA4 CU (MFMA issue, LDS bandwidth, L2→CU bandwidth), the wave
-// quantisation of the grid over 256 CUs and the HBM floor, and picks the
-// cheapest. Pure host code: no device needed.
+// M1 Pro. This one is a table measured on an MI355X for decide's engine
+// shapes, with a calibrated cost model (rounds of 256 workgroups, per-stage
+// time per tile height, HBM floor, split-K reduction) for every other shape.
+// Pure host code: no device needed.
 #pragma once
 
 #include <stdint.h>
@@ -28,7 +28,7 @@ double plan_estimate_us(int variant, uint32_t splits, uint32_t m, uint32_t n, ui
 Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
 // Best plan for a single GEMM. `max_ws` caps the split-K workspace bytes.
 Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws);
-// Best variant for a grouped launch of total width n_total (no split-K).
+// Best plan for a grouped launch of total width n_total (no split-K).
 Plan plan_grouped(uint32_t m, uint32_t n_total, uint32_t k);
 
 }  // namespace dh
