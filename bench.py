@@ -45,7 +45,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--report", action="store_true", help="also print per-shape GEMM timings to stderr")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="before timing, copy one gate|up weight copy (94,371,840 bytes) device to device: the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes")
     return ap.parse_args()
 
 
@@ -123,6 +125,11 @@ def main():
     res.copy_(x0)
     k.gemm.warm_up(stream, max_m=M)
     st.synchronize()
+    if args.calibration_copy:
+        calib = DeviceArray((2 * F, D), np.float16)
+        calib.copy_(wgu[0])
+        hip.synchronize()
+        calib.free()
     base_loaded = k.gemm.fast_pipelines()
 
     def step(i, ev=None):
