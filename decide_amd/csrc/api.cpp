@@ -348,7 +348,8 @@ int dh_final_head(dh_ctx* ctx, void* stream, const float* x, const float* w, con
                   uint32_t max_cand, float eps) {
   if (hidden == 0 || hidden % 8 != 0 || hidden > 16384)
     return fail(DH_EINVAL, "final_head: hidden = %u must be a positive multiple of 8, at most 16384", hidden);
-  if (max_cand < 1) return fail(DH_EINVAL, "final_head: max_cand must be at least 1");
+  if (max_cand < 1 || max_cand > 524280u)
+    return fail(DH_EINVAL, "final_head: max_cand = %u must be in 1..524280", max_cand);
   if (!aligned(table, 16)) return fail(DH_EINVAL, "final_head: table address %p must be a multiple of 16", table);
   if (!(eps > 0.0f)) return fail(DH_EINVAL, "final_head: eps must be positive");
   if (!ctx) return fail(DH_EINVAL, "final_head: null context");

@@ -112,7 +112,7 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
       const h8 o = *(const h8*)(st + row * LDH + oq * 8);
       _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + oq * 8;
       if (vec16) {
-        *(h8*)dst = o;
+        __builtin_nontemporal_store(o, (h8*)dst);  // streamed out: nothing re-reads it in this kernel
       } else {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
@@ -135,39 +135,6 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
         for (int e = 0; e < 4; ++e)
           stage[(i * 16 - c0 + 4 * g + e) * LDR + wave * 16 * FN + j * 16 + r] = acc[i][j][e];
     __syncthreads();
-    if (epi == 3u && !partial) {
-      // 8 fp16 outputs per item: output chunk oq of the tile row (16 per row)
-      constexpr int OQ = BN / 16;  // output chunks of 8 halves per row
-#pragma unroll
-      for (int it = 0; it < (rows * OQ + 255) / 256; ++it) {
-        const int item = it * 256 + tid;
-        if (item >= rows * OQ) break;
-        const int row = item / OQ, oq = item % OQ;
-        const uint32_t grow = m0 + c0 + row;
-        const uint32_t gcol = n0 + 32 * (oq / 2) + (oq % 2) * 8;  // first gate column
-        if (grow >= M || gcol >= N) continue;
-        const float* gp = stage + row * LDR + 32 * (oq / 2) + (oq % 2) * 8;
-        const f4 ga = *(const f4*)gp, gb = *(const f4*)(gp + 4);
-        const f4 ua = *(const f4*)(gp + 16), ub = *(const f4*)(gp + 20);
-        h8 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          o[q] = (_Float16)(silu_f(ga[q]) * ua[q]);
-          o[q + 4] = (_Float16)(silu_f(gb[q]) * ub[q]);
-        }
-        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + oq * 8;
-        if (vec16) {
-          *(h8*)dst = o;
-        } else {
-#pragma unroll
-          for (int q = 0; q < 8; q += 2) {
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            *(h2*)(dst + q) = h2{o[q], o[q + 1]};
-          }
-        }
-      }
-      return;
-    }
     // one float4 of a tile row per item; a wave covers one whole 256-column row
 #pragma unroll
     for (int it = 0; it < (rows * (BN / 4) + 255) / 256; ++it) {
@@ -178,7 +145,7 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
       if (grow >= M || gcol >= N) continue;
       const f4 v = *(const f4*)(stage + row * LDR + 4 * cq);
       if (partial) {
-        *(f4*)(p.ws + ((size_t)split * M + grow) * N + gcol) = v;
+        __builtin_nontemporal_store(v, (f4*)(p.ws + ((size_t)split * M + grow) * N + gcol));
       } else if (epi == 1u) {
         _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + gcol;
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));

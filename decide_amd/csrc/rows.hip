@@ -4,7 +4,7 @@
 //
 // decide counterparts: kernels/head.metal:8-59 (gather_rows_f32/f16,
 // final_head), kernels/rmsnorm.metal:8-30 (rmsnorm_rows). All are HBM- or
-// latency-bound; one workgroup per row, wave64 shuffles for the reductions.
+// latency-bound; wave64 shuffles for the reductions.
 #include "dh_kernels.h"
 
 namespace dh {
@@ -59,9 +59,15 @@ hipError_t launch_gather_rows(const void* x, const uint32_t* rowmap, void* out, 
 }
 
 // ---------------------------------------------------------------------------
-// Candidate head: one 256-thread workgroup per answer row. The normed row is
-// kept in LDS as fp32; each wave then takes candidates c = wave, wave + 4, …
-// and streams that bf16 table row with 16-byte loads.
+// Candidate head. Workgroup (r, q) serves answer row r, candidates
+// 8q .. 8q + 7: it recomputes the row's RMSNorm into LDS (fp32, cheap next to
+// the table reads), then each wave takes two candidates and streams both bf16
+// table rows with 16-byte loads, interleaved so two rows' loads are in flight.
+// Splitting the candidates over workgroups puts rows × ⌈max_cand / 8⌉
+// workgroups on the chip instead of one per row. Every candidate's sum is
+// formed in the same order whatever the split (lane-strided, then a wave sum).
+constexpr uint32_t kHeadCandPerGroup = 8;
+
 __global__ __launch_bounds__(256) void final_head_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                          const uint16_t* __restrict__ table,
                                                          const uint32_t* __restrict__ cand,
@@ -71,6 +77,9 @@ __global__ __launch_bounds__(256) void final_head_kernel(const float* __restrict
   extern __shared__ float hn[];  // [hidden]
   __shared__ float sh[4];
   const uint32_t r = blockIdx.x;
+  const uint32_t n = min(ncand[r], max_cand);
+  const uint32_t c0 = blockIdx.y * kHeadCandPerGroup;
+  if (c0 >= n) return;  // uniform over the workgroup
   const float* xr = x + (size_t)r * hidden;
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < hidden; i += 256) {
@@ -80,22 +89,31 @@ __global__ __launch_bounds__(256) void final_head_kernel(const float* __restrict
   const float inv = rsqrtf(block_sum256(ss, sh) / (float)hidden + eps);
   for (uint32_t i = threadIdx.x; i < hidden; i += 256) hn[i] = xr[i] * inv * (1.0f + w[i]);
   __syncthreads();
-  const uint32_t n = min(ncand[r], max_cand);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (uint32_t c = wave; c < n; c += 4) {
-    const uint16_t* er = table + (size_t)cand[(size_t)r * max_cand + c] * hidden;
-    float acc = 0.f;
-    for (uint32_t i = lane * 8; i < hidden; i += 64 * 8) {
-      const uint4 v = *(const uint4*)(er + i);
-      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t ca = c0 + 2 * wave, cb = ca + 1;
+  if (ca >= n) return;
+  const bool two = cb < n;
+  const uint16_t* ea = table + (size_t)cand[(size_t)r * max_cand + ca] * hidden;
+  const uint16_t* eb = two ? table + (size_t)cand[(size_t)r * max_cand + cb] * hidden : ea;
+  float acc_a = 0.f, acc_b = 0.f;
+  for (uint32_t i = lane * 8; i < hidden; i += 64 * 8) {
+    const uint4 va = *(const uint4*)(ea + i);
+    const uint4 vb = *(const uint4*)(eb + i);
+    const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc += hn[i + 2 * q] * bf16_to_f32((uint16_t)(wv[q] & 0xffffu));
-        acc += hn[i + 2 * q + 1] * bf16_to_f32((uint16_t)(wv[q] >> 16));
-      }
+    for (int q = 0; q < 4; ++q) {
+      const float h0 = hn[i + 2 * q], h1 = hn[i + 2 * q + 1];
+      acc_a += h0 * bf16_to_f32((uint16_t)(wa[q] & 0xffffu));
+      acc_a += h1 * bf16_to_f32((uint16_t)(wa[q] >> 16));
+      acc_b += h0 * bf16_to_f32((uint16_t)(wb[q] & 0xffffu));
+      acc_b += h1 * bf16_to_f32((uint16_t)(wb[q] >> 16));
     }
-    acc = wave_sum(acc);
-    if (lane == 0) logits[(size_t)r * max_cand + c] = acc;
+  }
+  acc_a = wave_sum(acc_a);
+  acc_b = wave_sum(acc_b);
+  if (lane == 0) {
+    logits[(size_t)r * max_cand + ca] = acc_a;
+    if (two) logits[(size_t)r * max_cand + cb] = acc_b;
   }
 }
 
@@ -103,8 +121,9 @@ hipError_t launch_final_head(const float* x, const float* w, const uint16_t* tab
                              const uint32_t* ncand, float* logits, uint32_t rows, uint32_t hidden, uint32_t max_cand,
                              float eps, hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(final_head_kernel, dim3(rows), dim3(256), hidden * sizeof(float), s, x, w, table, cand, ncand,
-                     logits, hidden, max_cand, eps);
+  const uint32_t groups = (max_cand + kHeadCandPerGroup - 1) / kHeadCandPerGroup;
+  hipLaunchKernelGGL(final_head_kernel, dim3(rows, groups), dim3(256), hidden * sizeof(float), s, x, w, table, cand,
+                     ncand, logits, hidden, max_cand, eps);
   return hipGetLastError();
 }
 

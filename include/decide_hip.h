@@ -130,7 +130,7 @@ int dh_gather_rows_f16(dh_ctx* ctx, void* stream, const uint16_t* x, const uint3
  * bf16 rows of `table` [vocab, hidden] named by cand[r * max_cand + c] for
  * c < min(ncand[r], max_cand). Writes logits[r * max_cand + c]; entries past
  * ncand[r] are left untouched. decide fixes hidden = 2560 and max_cand = 62;
- * here both are parameters (hidden % 8 == 0, hidden <= 16384, max_cand >= 1).
+ * here both are parameters (hidden % 8 == 0, hidden <= 16384, 1 <= max_cand <= 524280).
  * Candidate ids >= vocab are a contract violation the kernel cannot see: the
  * caller validates ids (decide: forward.rs:1494-1537). */
 int dh_final_head(dh_ctx* ctx, void* stream, const float* x, const float* w, const uint16_t* table,

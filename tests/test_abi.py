@@ -88,6 +88,8 @@ def test_final_head_contract():
     assert rc == _lib.DH_EINVAL and "multiple of 8" in _lib.last_error()
     rc = lib.dh_final_head(None, None, 16, 16, 16, 16, 16, 16, 3, 2560, 0, 1e-6)
     assert rc == _lib.DH_EINVAL and "max_cand" in _lib.last_error()
+    rc = lib.dh_final_head(None, None, 16, 16, 16, 16, 16, 16, 3, 2560, 524281, 1e-6)
+    assert rc == _lib.DH_EINVAL and "max_cand" in _lib.last_error()
 
 
 def test_grouped_member_errors_name_the_member():

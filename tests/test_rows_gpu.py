@@ -55,7 +55,8 @@ def test_gather_bf16_candidate_rows_from_a_151936_vocab(gpu, kernels, stream):
     assert np.array_equal(to_host(out), t[ids])
 
 
-@pytest.mark.parametrize("rows,hidden,max_cand", [(24, 2560, 64), (3, 2560, 8), (6, 256, 8), (16, 2560, 62)])
+@pytest.mark.parametrize("rows,hidden,max_cand", [(24, 2560, 64), (3, 2560, 8), (6, 256, 8), (16, 2560, 62),
+                                                    (5, 2560, 13), (4, 512, 1), (7, 1024, 17)])
 def test_final_head_matches_oracle(gpu, kernels, stream, rows, hidden, max_cand):
     vocab = 151936 if hidden == 2560 else 1000
     x = synth.normal_f32(synth.seed_for(90), (rows, hidden), 3.0)
