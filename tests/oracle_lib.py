@@ -25,8 +25,8 @@ def load() -> ctypes.CDLL:
     global _lib
     if _lib is not None:
         return _lib
-    src = os.path.join(ORACLE_DIR, "oracle.c")
-    if not os.path.exists(ORACLE_SO) or os.path.getmtime(ORACLE_SO) < os.path.getmtime(src):
+    srcs = [os.path.join(ORACLE_DIR, f) for f in ("oracle.c", "oracle_mixer.c", "Makefile")]
+    if not os.path.exists(ORACLE_SO) or os.path.getmtime(ORACLE_SO) < max(os.path.getmtime(f) for f in srcs):
         subprocess.run(["make", "-C", ORACLE_DIR], check=True, capture_output=True)
     lib = ctypes.CDLL(ORACLE_SO)
     sig = {
@@ -55,6 +55,16 @@ def load() -> ctypes.CDLL:
         "orc_gemm_f32_fast": (None, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_int]),
         "orc_rel_frobenius": (c_double, [c_void_p, c_void_p, c_size_t]),
         "orc_assert_close": (c_int64, [c_void_p, c_void_p, c_size_t, c_float, c_float]),
+        "orc_softplus": (c_float, [c_float]),
+        "orc_inv_freq": (None, [c_void_p]),
+        "orc_conv_silu_l2": (None, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+        "orc_conv_state_update": (None, [c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+        "orc_gated_delta": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,
+                                   c_void_p, c_uint32, c_void_p]),
+        "orc_gated_rmsnorm_silu": (None, [c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p]),
+        "orc_head_norm_rope": (None, [c_void_p, c_void_p, c_uint32, c_void_p]),
+        "orc_attention": (None, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
+        "orc_embed_bf16": (None, [c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -178,4 +188,84 @@ def f16_round(a: np.ndarray) -> np.ndarray:
     load().orc_f32_array_to_f16(_p(a), _p(bits), a.size)
     out = np.empty(a.shape, dtype=np.float32)
     load().orc_f16_array_to_f32(_p(bits), _p(out), a.size)
+    return out
+
+
+# ---- the non-GEMM forward pieces (oracle_mixer.c; cpu_ref.rs:55-188)
+NK, DK, NV, DV = 16, 128, 32, 128
+KEY_DIM, VALUE_DIM, CONV_DIM = NK * DK, NV * DV, 2 * NK * DK + NV * DV
+NQ, NKV, HEAD_DIM = 16, 4, 256
+Q_DIM, KV_DIM = NQ * HEAD_DIM, NKV * HEAD_DIM
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def softplus(x: float) -> float:
+    return float(load().orc_softplus(x))
+
+
+def inv_freq() -> np.ndarray:
+    out = np.empty(32, np.float32)
+    load().orc_inv_freq(_p(out))
+    return out
+
+
+def conv_silu_l2(p: np.ndarray, t: int, prev: np.ndarray, w: np.ndarray):
+    """cpu_ref::conv_silu_l2 over the first CONV_DIM columns of p [t, ldp] → (q [t,16,128], k, v [t,32,128])."""
+    p, prev, w = _f32(p), _f32(prev), _f32(w)
+    q = np.empty((t, NK, DK), np.float32)
+    k = np.empty((t, NK, DK), np.float32)
+    v = np.empty((t, NV, DV), np.float32)
+    load().orc_conv_silu_l2(_p(p), p.shape[1], t, _p(prev), _p(w), _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def conv_state_update(p: np.ndarray, t: int, prev: np.ndarray) -> np.ndarray:
+    p, prev = _f32(p), _f32(prev)
+    out = np.empty((3, CONV_DIM), np.float32)
+    load().orc_conv_state_update(_p(p), p.shape[1], t, _p(prev), _p(out))
+    return out
+
+
+def gated_delta(q, k, v, a, b, a_log, dt_bias, state, t: int):
+    """cpu_ref::gated_delta; a, b are [t, ldab] (head h at column h). Returns (o [t,32,128], new state)."""
+    q, k, v, a, b = _f32(q), _f32(k), _f32(v), _f32(a), _f32(b)
+    st = _f32(state).copy()
+    o = np.empty((t, NV, DV), np.float32)
+    load().orc_gated_delta(_p(q), _p(k), _p(v), _p(a), _p(b), a.shape[1], _p(_f32(a_log)), _p(_f32(dt_bias)),
+                           _p(st), t, _p(o))
+    return o, st
+
+
+def gated_rmsnorm_silu(o, z, w, t: int) -> np.ndarray:
+    o, z, w = _f32(o), _f32(z), _f32(w)
+    y = np.empty((t, VALUE_DIM), np.float32)
+    load().orc_gated_rmsnorm_silu(_p(o), _p(z), z.shape[1], _p(w), t, _p(y))
+    return y
+
+
+def head_norm_rope(seg, w, pos: int) -> np.ndarray:
+    seg, w = _f32(seg), _f32(w)
+    out = np.empty(HEAD_DIM, np.float32)
+    load().orc_head_norm_rope(_p(seg), _p(w), pos, _p(out))
+    return out
+
+
+def attention(q, qpos, kc, vc, gate) -> np.ndarray:
+    """cpu_ref::attention: q [rows,16,256], kc/vc [npos,4,256], gate [rows, ldg] → [rows, 4096]."""
+    q, kc, vc, gate = _f32(q), _f32(kc), _f32(vc), _f32(gate)
+    qpos = np.ascontiguousarray(qpos, dtype=np.uint32)
+    rows = len(qpos)
+    out = np.empty((rows, Q_DIM), np.float32)
+    load().orc_attention(_p(q), _p(qpos), rows, _p(kc), _p(vc), _p(gate), gate.shape[1], _p(out))
+    return out
+
+
+def embed_bf16(ids, table_bits) -> np.ndarray:
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    table_bits = np.ascontiguousarray(table_bits, dtype=np.uint16)
+    out = np.empty((len(ids), table_bits.shape[1]), np.float32)
+    load().orc_embed_bf16(_p(ids), _p(table_bits), len(ids), table_bits.shape[1], _p(out))
     return out
