@@ -89,6 +89,30 @@ PROTOTYPES = {
     "dh_interleave_gate_up": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
     "dh_deinterleave_q_gate": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
     "dh_bf16_to_f16": (c_int, [c_void_p, c_void_p, c_uint64, POINTER(c_uint64)]),
+    "dh_embed_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+    "dh_conv_silu_l2": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32],
+    ),
+    "dh_conv_state_update": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+    "dh_gated_delta": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_uint32, c_uint32, c_uint32],
+    ),
+    "dh_gated_rmsnorm_silu": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+    "dh_q_norm_rope": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]),
+    "dh_kv_norm_rope": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
+         c_uint32, c_uint32],
+    ),
+    "dh_attention": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32],
+    ),
+    "dh_fill_normal": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_float, c_float, c_uint32]),
 }
 
 _lib = None

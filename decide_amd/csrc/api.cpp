@@ -16,27 +16,13 @@
 #include <string>
 
 #include "../../include/decide_hip.h"
+#include "api_internal.h"
 #include "dh_kernels.h"
 #include "plan.h"
 
-struct dh_ctx {
-  uint32_t flags = 0;
-  int device = 0;
-  std::mutex ws_lock;
-  float* ws = nullptr;
-  uint64_t ws_bytes = 0;
-  uint64_t ws_cap = 512ull << 20;  // split-K workspace ceiling
-  int forced_variant = -1;
-  uint32_t forced_splits = 0;
-  std::atomic<uint64_t> used{0};  // bit per distinct kernel launched
-};
-
-namespace {
+namespace dh_api {
 
 thread_local std::string g_err;
-
-// Kernel ids for dh_variants_loaded beyond the tile menu.
-enum : int { kKidReduce = 48, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill };
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -61,6 +47,12 @@ int hip_status(hipError_t e, const char* what) {
 void mark(dh_ctx* c, int kid) { c->used.fetch_or(1ull << kid, std::memory_order_relaxed); }
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace dh_api
+
+using namespace dh_api;
+
+namespace {
 
 // gemm.rs:140-144 and 159-163.
 int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const void* y, uint32_t ldy, uint32_t m,

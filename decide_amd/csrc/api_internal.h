@@ -1,0 +1,43 @@
+// Shared by the C-ABI translation units: the context object and the
+// status/error helpers (dh_last_error's per-thread message).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <mutex>
+
+#include "../../include/decide_hip.h"
+
+struct dh_ctx {
+  uint32_t flags = 0;
+  int device = 0;
+  std::mutex ws_lock;
+  float* ws = nullptr;
+  uint64_t ws_bytes = 0;
+  uint64_t ws_cap = 512ull << 20;  // split-K workspace ceiling
+  int forced_variant = -1;
+  uint32_t forced_splits = 0;
+  std::atomic<uint64_t> used{0};  // bit per distinct kernel launched
+};
+
+namespace dh_api {
+
+// Kernel ids for dh_variants_loaded beyond the tile menu (ids < 48).
+enum : int {
+  kKidReduce = 48, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
+  kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny
+};
+
+// Records `fmt` as the thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the thread's last error and returns DH_OK.
+int ok();
+// DH_OK, or DH_ELAUNCH with `what` and HIP's message.
+int hip_status(hipError_t e, const char* what);
+// Records that kernel `kid` has been launched through this context.
+void mark(dh_ctx* c, int kid);
+bool aligned(const void* p, uintptr_t a);
+
+}  // namespace dh_api

@@ -1,0 +1,174 @@
+// Causal GQA attention with the sigmoid output gate, for gfx950 MFMA
+// (decide: kernels/attn_fast.metal; cpu_ref.rs:167-188):
+//   y[r, h·256 + d] = (softmax_j(q_r,h · k_j,h/4 / 16) · v_·,h/4)[d] · σ(gate[r, h·256 + d]),
+// over cache rows j = 0 ..= qpos[r]; q, K, V fp16, scores and softmax fp32,
+// the softmax weights rounded to fp16 once as the P·V operand, y fp16.
+//
+// Design (MI355X's own):
+//   * A workgroup is one kv head × 16 query rows; its 4 waves are the 4 query
+//     heads sharing that kv head, so one staged K/V tile serves all four.
+//   * Everything is computed transposed: Sᵀ = K·Qᵀ (A = K rows from LDS,
+//     B = the wave's Q rows held in registers for the whole kernel) and
+//     Oᵀ += Vᵀ·Pᵀ. In the MFMA output layout a lane then holds 8 scores of
+//     ONE query row for keys {4g..4g+3, 16+4g..16+4g+3} (g = lane / 16), which
+//     is exactly the B operand Pᵀ needs if the 32 keys of a block are taken
+//     in that order — so P goes from scores to MFMA operand without leaving
+//     registers. Vᵀ is staged key-contiguous (transposed on the way into LDS)
+//     and read in the same key order.
+//   * Online softmax in the exp2 domain; a row's max is reduced across the
+//     four lane groups that hold it (two xor shuffles); the running sum stays
+//     per lane and is reduced once at the end. O is rescaled only when some
+//     row's max moved.
+//   * Query blocks run longest-first so the causal triangle's tail is not
+//     the last work scheduled. Rows past `rows` are clamped for loads and
+//     skipped for stores; keys past the block's last position are masked
+//     (their staged rows are clamped reads of valid cache rows).
+#include "dh_kernels.h"
+
+namespace dh {
+
+namespace {
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHD = 256, kNQ = 16, kQDim = kNQ * kHD;
+constexpr int kBQ = 16;    // query rows per workgroup
+constexpr int kBKey = 32;  // keys per block
+constexpr int kKLD = kHD + 8;  // K tile row stride (halves): 528 B, conflict-free 16-lane reads
+constexpr int kVLD = kBKey + 8;  // Vᵀ tile row stride (halves): 80 B
+constexpr float kScaleLog2 = 0.0625f * 1.4426950408889634f;  // 1/16 · log2(e)
+constexpr float kNeg = -1e30f;
+
+__device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+}  // namespace
+
+__global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ kc,
+                                                        const _Float16* __restrict__ vc, const float* __restrict__ pq,
+                                                        const uint32_t* __restrict__ qpos, _Float16* __restrict__ y,
+                                                        uint32_t ldq, uint32_t rows) {
+  __shared__ __attribute__((aligned(16))) _Float16 ks[kBKey * kKLD];
+  __shared__ __attribute__((aligned(16))) _Float16 vts[kHD * kVLD];
+  const uint32_t qb = gridDim.x - 1 - blockIdx.x;
+  const uint32_t kvh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t h = kvh * 4 + wave;
+  const int rl = lane & 15, g = lane >> 4;
+  const uint32_t r0 = qb * kBQ;
+  const uint32_t row = min(r0 + rl, rows - 1);
+  const uint32_t mypos = qpos[row];
+  uint32_t pmax = mypos;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) pmax = max(pmax, (uint32_t)__shfl_xor((int)pmax, o, 64));
+
+  h8 qf[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) qf[c] = *(const h8*)(q + ((size_t)row * kNQ + h) * kHD + 32 * c + 8 * g);
+  f4 oacc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) oacc[i] = f4{0.f, 0.f, 0.f, 0.f};
+  float m = kNeg, lsum = 0.f;
+
+  const uint32_t nblk = pmax / kBKey + 1;
+  const int kq = tid & 7, dc = tid >> 3;  // V staging: key quad, 8-dim chunk
+  for (uint32_t blk = 0; blk < nblk; ++blk) {
+    const uint32_t kb0 = blk * kBKey;
+    __syncthreads();  // the previous block's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = tid + 256 * i, key = id >> 5, c16 = id & 31;
+      const uint32_t src = min(kb0 + key, pmax);
+      *(h8*)(ks + key * kKLD + 8 * c16) = *(const h8*)(kc + ((size_t)src * 4 + kvh) * kHD + 8 * c16);
+    }
+    {
+      h8 vv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t src = min(kb0 + 4 * kq + e, pmax);
+        vv[e] = *(const h8*)(vc + ((size_t)src * 4 + kvh) * kHD + 8 * dc);
+      }
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        *(h4*)(vts + (8 * dc + d) * kVLD + 4 * kq) = h4{vv[0][d], vv[1][d], vv[2][d], vv[3][d]};
+    }
+    __syncthreads();
+
+    f4 st[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) st[kt] = mfma16(*(const h8*)(ks + (16 * kt + rl) * kKLD + 32 * c + 8 * g), qf[c], st[kt]);
+
+    float sv[8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t key = kb0 + 16 * kt + 4 * g + e;
+        sv[4 * kt + e] = key <= mypos ? st[kt][e] * kScaleLog2 : kNeg;
+      }
+    float bm = sv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, sv[i]);
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mnew = fmaxf(m, bm);
+    const float alpha = exp2f(m - mnew);
+    h8 pb;
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float pv = exp2f(sv[i] - mnew);
+      ps += pv;
+      pb[i] = (_Float16)pv;
+    }
+    lsum = lsum * alpha + ps;
+    m = mnew;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[i] *= alpha;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const _Float16* vr = vts + (16 * dt + rl) * kVLD + 4 * g;
+      const h4 lo = *(const h4*)vr, hi = *(const h4*)(vr + 16);
+      const h8 va = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      oacc[dt] = mfma16(va, pb, oacc[dt]);
+    }
+  }
+
+  float l = lsum + __shfl_xor(lsum, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const float inv = 1.0f / l;
+  if (r0 + rl < rows) {
+    const uint32_t r = r0 + rl;
+    const float* gp = pq + (size_t)r * ldq + kQDim + h * kHD;
+    _Float16* yp = y + (size_t)r * kQDim + h * kHD;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const int d0 = 16 * dt + 4 * g;
+      // gate as two float2 and y as two half2: 8- and 4-byte alignment suffice (decide's contract)
+      const f2 g01 = *(const f2*)(gp + d0), g23 = *(const f2*)(gp + d0 + 2);
+      const float gt[4] = {g01[0], g01[1], g23[0], g23[1]};
+      _Float16 o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (_Float16)(oacc[dt][e] * inv * (1.0f / (1.0f + __expf(-gt[e]))));
+      *(h2*)(yp + d0) = h2{o[0], o[1]};
+      *(h2*)(yp + d0 + 2) = h2{o[2], o[3]};
+    }
+  }
+}
+
+hipError_t launch_attention(const _Float16* q, const _Float16* kc, const _Float16* vc, const float* pq,
+                            const uint32_t* qpos, _Float16* y, uint32_t rows, uint32_t ldq, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(attention_kernel, dim3((rows + kBQ - 1) / kBQ, 4), dim3(256), 0, s, q, kc, vc, pq, qpos, y, ldq,
+                     rows);
+  return hipGetLastError();
+}
+
+}  // namespace dh

@@ -64,5 +64,27 @@ hipError_t launch_final_head(const float* x, const float* w, const uint16_t* tab
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, _Float16* y, const uint32_t* rowmap, uint32_t rows,
                                uint32_t h, uint32_t ld_in, uint32_t ld_out, bool add_one, float eps, hipStream_t s);
 hipError_t launch_fill_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float std, hipStream_t s);
+hipError_t launch_fill_normal(void* out, uint64_t n, uint64_t seed, float mean, float sd, uint32_t dtype,
+                              hipStream_t s);
+
+// ---- the non-GEMM forward kernels (mixer.hip, attention.hip)
+hipError_t launch_conv_silu_l2(const float* p, const float* prev, const float* w, float* q, float* k, float* v,
+                               uint32_t t, uint32_t ldp, hipStream_t s);
+hipError_t launch_conv_state_update(const float* p, const float* prev_in, float* prev_out, uint32_t t, uint32_t ldp,
+                                    hipStream_t s);
+hipError_t launch_gated_delta(const float* q, const float* k, const float* v, const float* a, const float* b,
+                              const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
+                              float* o, uint32_t t, uint32_t ldab, bool write_state, hipStream_t s);
+hipError_t launch_gated_rmsnorm_silu(const float* o, const float* z, const float* w, _Float16* y, uint32_t t,
+                                     uint32_t ldz, hipStream_t s);
+hipError_t launch_q_norm_rope(const float* pq, const float* qw, const float* inv_freq, const uint32_t* qpos,
+                              _Float16* qo, uint32_t rows, uint32_t ldq, hipStream_t s);
+hipError_t launch_kv_norm_rope(const float* pkv, const float* kw, const float* inv_freq, _Float16* kc, _Float16* vc,
+                               uint32_t rows, uint32_t ldkv, uint32_t kcol, uint32_t vcol, uint32_t pos0,
+                               hipStream_t s);
+hipError_t launch_attention(const _Float16* q, const _Float16* kc, const _Float16* vc, const float* pq,
+                            const uint32_t* qpos, _Float16* y, uint32_t rows, uint32_t ldq, hipStream_t s);
+hipError_t launch_embed_bf16(const uint32_t* ids, const uint16_t* table, float* out, uint32_t t, uint32_t h,
+                             hipStream_t s);
 
 }  // namespace dh

@@ -192,16 +192,114 @@ class Norm:
                                        addr(rowmap), rows, h, ld_in, ld_out, 1 if add_one else 0, eps))
 
 
+class Embed:
+    """decide's ``Embed`` (kernels/embed.rs:11-24)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def embed(self, stream: int, ids: Arg, table: Arg, out: Arg, t: int, h: int = 2560) -> None:
+        """out[t] = embed[ids[t]] (bf16 → f32), rows [t, h]."""
+        _call(self.lib.dh_embed_bf16(self.ctx.handle, ctypes.c_void_p(stream), addr(ids), addr(table), addr(out), t,
+                                     h))
+
+
+class Conv:
+    """decide's ``Conv`` (kernels/conv.rs:11-48)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def conv_silu_l2(self, stream: int, p: Arg, prev: Arg, w: Arg, q: Arg, k: Arg, v: Arg, t: int, ldp: int) -> None:
+        _call(self.lib.dh_conv_silu_l2(self.ctx.handle, ctypes.c_void_p(stream), addr(p), addr(prev), addr(w),
+                                       addr(q), addr(k), addr(v), t, ldp))
+
+    def conv_state_update(self, stream: int, p: Arg, prev_in: Arg, prev_out: Arg, t: int, ldp: int) -> None:
+        _call(self.lib.dh_conv_state_update(self.ctx.handle, ctypes.c_void_p(stream), addr(p), addr(prev_in),
+                                            addr(prev_out), t, ldp))
+
+
+class Delta:
+    """decide's ``Delta`` (kernels/delta.rs:28-80)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def gated_delta(self, stream: int, q: Arg, k: Arg, v: Arg, a: Arg, b: Arg, a_log: Arg, dt_bias: Arg,
+                    state_in: Arg, state_out: Arg, o: Arg, t: int, ldab: int, write_state: bool) -> None:
+        _call(self.lib.dh_gated_delta(self.ctx.handle, ctypes.c_void_p(stream), addr(q), addr(k), addr(v), addr(a),
+                                      addr(b), addr(a_log), addr(dt_bias), addr(state_in), addr(state_out), addr(o),
+                                      t, ldab, 1 if write_state else 0))
+
+
+class GNorm:
+    """decide's ``GNorm`` (kernels/gnorm.rs:10-31)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def gated_rmsnorm_silu(self, stream: int, o: Arg, z: Arg, w: Arg, y: Arg, t: int, ldz: int) -> None:
+        _call(self.lib.dh_gated_rmsnorm_silu(self.ctx.handle, ctypes.c_void_p(stream), addr(o), addr(z), addr(w),
+                                             addr(y), t, ldz))
+
+
+class Rope:
+    """decide's ``Rope`` (kernels/rope.rs:16-54)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def q_norm_rope(self, stream: int, pq: Arg, qw: Arg, inv_freq: Arg, qpos: Arg, qo: Arg, rows: int,
+                    ldq: int) -> None:
+        _call(self.lib.dh_q_norm_rope(self.ctx.handle, ctypes.c_void_p(stream), addr(pq), addr(qw), addr(inv_freq),
+                                      addr(qpos), addr(qo), rows, ldq))
+
+    def kv_norm_rope(self, stream: int, pkv: Arg, kw: Arg, inv_freq: Arg, kc: Arg, vc: Arg, rows: int, ldkv: int,
+                     kcol: int, vcol: int, pos0: int) -> None:
+        _call(self.lib.dh_kv_norm_rope(self.ctx.handle, ctypes.c_void_p(stream), addr(pkv), addr(kw), addr(inv_freq),
+                                       addr(kc), addr(vc), rows, ldkv, kcol, vcol, pos0))
+
+
+class Attn:
+    """decide's ``Attn`` (kernels/attn.rs:44-125)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.lib = ctx.lib
+
+    def attention(self, stream: int, q: Arg, kc: Arg, vc: Arg, pq: Arg, qpos: Arg, y: Arg, rows: int,
+                  ldq: int) -> None:
+        _call(self.lib.dh_attention(self.ctx.handle, ctypes.c_void_p(stream), addr(q), addr(kc), addr(vc), addr(pq),
+                                    addr(qpos), addr(y), rows, ldq))
+
+
+def fill_normal(ctx: Context, stream: int, out: Arg, n: int, seed: int, mean: float, std: float, dtype: str) -> None:
+    """N(mean, std) fill of fp16 / bf16 / fp32 values from the counter-based generator."""
+    code = {"f16": 0, "bf16": 1, "f32": 2}[dtype]
+    _call(ctx.lib.dh_fill_normal(ctx.handle, ctypes.c_void_p(stream), addr(out), n, seed, mean, std, code))
+
+
 def fill_normal_f16(ctx: Context, stream: int, out: Arg, n: int, seed: int, std: float) -> None:
     """N(0, std) fp16 fill from a counter-based generator (reproducible per (seed, index))."""
     _call(ctx.lib.dh_fill_normal_f16(ctx.handle, ctypes.c_void_p(stream), addr(out), n, seed, std))
 
 
 class Kernels:
-    """decide's ``Kernels`` registry (kernels/mod.rs:40-67), restricted to the GEMM path."""
+    """decide's ``Kernels`` registry (kernels/mod.rs:40-67): the GEMM path and the forward kernels beside it."""
 
     def __init__(self, imp: GemmImpl = GemmImpl.Fast):
         self.ctx = Context(imp)
         self.gemm = Gemm(self.ctx)
         self.head = Head(self.ctx)
         self.norm = Norm(self.ctx)
+        self.embed = Embed(self.ctx)
+        self.conv = Conv(self.ctx)
+        self.delta = Delta(self.ctx)
+        self.gnorm = GNorm(self.ctx)
+        self.rope = Rope(self.ctx)
+        self.attn = Attn(self.ctx)

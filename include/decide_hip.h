@@ -167,6 +167,81 @@ int dh_deinterleave_q_gate(const uint16_t* src, uint16_t* out, uint32_t heads, u
  * counts[0..3] = {values, subnormal, flushed to zero, overflow} if non-NULL. */
 int dh_bf16_to_f16(const uint16_t* src, uint16_t* out, uint64_t n, uint64_t* counts);
 
+/* ======================================================================
+ * Forward kernels beside the GEMMs: the non-GEMM steps of decide's hybrid
+ * decoder forward (forward.rs:1191-1254). Model constants are decide's
+ * (config.rs:4-31): 16 key heads and 32 value heads of 128 dims in the
+ * Gated-DeltaNet layers (CONV_DIM 8192 = q 2048 | k 2048 | v 4096), 16 query
+ * heads over 4 kv heads of 256 dims in the attention layers.
+ * ====================================================================== */
+
+/* decide: Embed::embed (kernels/embed.rs:17; kernels/embed.metal). out fp32
+ * [t, h] = the bf16 rows table[ids[i]] widened bitwise. h % 8 == 0, table and
+ * out 16-byte aligned. ids < vocab is the caller's check (forward.rs:1494-1537). */
+int dh_embed_bf16(dh_ctx* ctx, void* stream, const uint32_t* ids, const uint16_t* table, float* out, uint32_t t,
+                  uint32_t h);
+
+/* decide: Conv::conv_silu_l2 (kernels/conv.rs:20-35; cpu_ref::conv_silu_l2,
+ * cpu_ref.rs:55-81). Reads the qkv columns 0..8192 of t rows of p (fp32, row
+ * stride ldp) and prev, the 3 raw rows before them (fp32 [3, 8192], oldest
+ * first); w is fp32 [8192, 4]. Writes fp32 q, k [t, 16, 128] (L2-normed, q also
+ * scaled by 128^-1/2) and v [t, 32, 128]. ldp even and >= 8192; p, prev, q, k,
+ * v 8-byte and w 16-byte aligned. */
+int dh_conv_silu_l2(dh_ctx* ctx, void* stream, const float* p, const float* prev, const float* w, float* q, float* k,
+                    float* v, uint32_t t, uint32_t ldp);
+/* decide: Conv::conv_state_update (kernels/conv.rs:37-48; cpu_ref.rs:86-95).
+ * prev_out [3, 8192] = the raw qkv rows t-3, t-2, t-1 (from prev_in where
+ * negative). prev_out may be prev_in. */
+int dh_conv_state_update(dh_ctx* ctx, void* stream, const float* p, const float* prev_in, float* prev_out, uint32_t t,
+                         uint32_t ldp);
+
+/* decide: Delta::gated_delta (kernels/delta.rs:53-80; cpu_ref::gated_delta,
+ * cpu_ref.rs:101-129). fp32 throughout: q, k [t, 16, 128]; v, o [t, 32, 128];
+ * a, b rows of stride ldab (value head h at column h); a_log, dt_bias [32];
+ * state [32][128 dv][128 dk]. state_in may be state_out; with write_state 0
+ * state_out is not written (and may be NULL). t >= 1, ldab >= 32; q, k and the
+ * states 16-byte aligned. */
+int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, const float* v, const float* a,
+                   const float* b, const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
+                   float* o, uint32_t t, uint32_t ldab, uint32_t write_state);
+
+/* decide: GNorm::gated_rmsnorm_silu (kernels/gnorm.rs:19-31; cpu_ref.rs:132-145).
+ * y fp16 [t, 4096] = per (row, value head) RMSNorm of o over 128 dims with
+ * weight w (fp32 [128], no +1), times silu(z); z rows of stride ldz. */
+int dh_gated_rmsnorm_silu(dh_ctx* ctx, void* stream, const float* o, const float* z, const float* w, uint16_t* y,
+                          uint32_t t, uint32_t ldz);
+
+/* decide: Rope::q_norm_rope (kernels/rope.rs:25-37; cpu_ref::head_norm_rope,
+ * cpu_ref.rs:149-162). For the 16 q heads (column 256 h) of rows of pq (fp32,
+ * row stride ldq): zero-centred RMSNorm with qw (fp32 [256], applied as 1 + w),
+ * RoPE on dims [0, 64) at position qpos[r] with inv_freq (fp32 [32]); writes
+ * fp16 qo [rows, 16, 256]. ldq % 4 == 0; pq, qw 16-byte and qo 8-byte aligned. */
+int dh_q_norm_rope(dh_ctx* ctx, void* stream, const float* pq, const float* qw, const float* inv_freq,
+                   const uint32_t* qpos, uint16_t* qo, uint32_t rows, uint32_t ldq);
+/* decide: Rope::kv_norm_rope (kernels/rope.rs:39-54). Row r at position
+ * pos0 + r: the 4 k heads at column kcol, normed and rotated like q, into the
+ * fp16 K cache kc [pos][4][256]; the 4 v heads at column vcol copied into the
+ * V cache vc. pos0 + rows <= 8192 (decide's MAX_TOKENS cache rows). */
+int dh_kv_norm_rope(dh_ctx* ctx, void* stream, const float* pkv, const float* kw, const float* inv_freq, uint16_t* kc,
+                    uint16_t* vc, uint32_t rows, uint32_t ldkv, uint32_t kcol, uint32_t vcol, uint32_t pos0);
+
+/* decide: Attn::attention (kernels/attn.rs:80-125; cpu_ref::attention,
+ * cpu_ref.rs:167-188). q fp16 [rows, 16, 256]; row r at position qpos[r]
+ * attends to cache rows 0..=qpos[r] of kc/vc (fp16 [pos][4][256]); the gate is
+ * read from pq (fp32, row stride ldq) at column 4096 + 256 h + d. y fp16
+ * [rows, 4096] = softmax(q·kᵀ/16)·v ⊙ σ(gate). rows >= 1, ldq >= 8192 and even;
+ * q, kc, vc 16-byte, pq 8-byte, qpos and y 4-byte aligned. Cache rows
+ * 0..=max(qpos) must hold finite values. */
+int dh_attention(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const float* pq,
+                 const uint32_t* qpos, uint16_t* y, uint32_t rows, uint32_t ldq);
+
+/* Random-init fill for every parameter dtype (the role of decide's
+ * testutil::uniform, testutil.rs:4-8, with the Gaussians BASELINE asks for):
+ * n values N(mean, std) as fp16 (dtype 0), bf16 (1) or fp32 (2), element i a
+ * function of (seed, i) only — the generator of dh_fill_normal_f16. */
+int dh_fill_normal(dh_ctx* ctx, void* stream, void* out, uint64_t n, uint64_t seed, float mean, float std,
+                   uint32_t dtype);
+
 #ifdef __cplusplus
 }
 #endif

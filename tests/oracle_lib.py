@@ -232,6 +232,7 @@ def conv_state_update(p: np.ndarray, t: int, prev: np.ndarray) -> np.ndarray:
 def gated_delta(q, k, v, a, b, a_log, dt_bias, state, t: int):
     """cpu_ref::gated_delta; a, b are [t, ldab] (head h at column h). Returns (o [t,32,128], new state)."""
     q, k, v, a, b = _f32(q), _f32(k), _f32(v), _f32(a), _f32(b)
+    assert a.shape == b.shape, "a and b share one row stride"
     st = _f32(state).copy()
     o = np.empty((t, NV, DV), np.float32)
     load().orc_gated_delta(_p(q), _p(k), _p(v), _p(a), _p(b), a.shape[1], _p(_f32(a_log)), _p(_f32(dt_bias)),
