@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-forward", action="store_true", help="skip the config-5 full forward timing")
+    ap.add_argument("--forward-runs", type=int, default=20, help="timed forwards per prompt length (p50)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="before timing, copy one gate|up weight copy (94,371,840 bytes) device to device: the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes")
@@ -94,6 +96,54 @@ def cpu_baseline(seconds: float):
         "sample": f"{rows_done} of {M} rows of the C2 MLP block (gate|up + SwiGLU + down), "
                   f"oracle cpu_ref::gemm_nt restatement, f64 sums, 1 thread, {elapsed:.1f} s",
     }
+
+
+def forward_timing(k, runs: int):
+    """the 4B-shaped hybrid forward (36 layers, 27 Gated-DeltaNet + 9 gated attention,
+    d 2560, d_ff 9216, vocab 151,936), random-init fp16 GEMM weights / bf16 embedding / fp32 small
+    parameters, a seeded uniform prompt, 3 answer rows × 8 candidates; p50 of `runs` forwards after 3
+    warm-ups (decide's bench: 3 warm-ups + 20 timed, p50 by linear interpolation, bench.rs:40-112), at
+    2,307 and at 603 tokens. Each forward is timed with HIP events around the whole enqueue on one stream
+    (embedding → candidate logits, decide's "forward" span less the host's id staging)."""
+    from decide_amd import hip, synth
+    from decide_amd.forward import Model, ModelConfig
+    from decide_amd.hip import DeviceArray, Event, Stream
+
+    cfg = ModelConfig(layers=36, vocab=151936, max_tokens=2307, max_answers=3, max_cand=8)
+    st = Stream()
+    s = st.handle
+    model = Model(k.ctx, cfg)
+    model.init_random(s, seed=0xDEC1DE)
+    k.gemm.warm_up(s, max_m=cfg.max_tokens)
+    st.synchronize()
+    out = {}
+    for t in (2307, 603):
+        ids = DeviceArray.from_numpy(synth.uniform_ids(synth.seed_for(500 + t), t, cfg.vocab).astype(np.uint32))
+        ans = DeviceArray.from_numpy(np.array([t - 3, t - 2, t - 1], np.uint32))
+        cand = DeviceArray.from_numpy(synth.uniform_ids(synth.seed_for(501 + t), 3 * 8, cfg.vocab).astype(np.uint32))
+        ncand = DeviceArray.from_numpy(np.full(3, 8, np.uint32))
+        logits = DeviceArray((3, 8), np.float32)
+        run = lambda: model.forward(s, (ids, 0), t, (ans, 0), 3, (cand, 0), (ncand, 0), (logits, 0))
+        for _ in range(3):
+            run()
+        st.synchronize()
+        times = []
+        for _ in range(runs):
+            e0, e1 = Event(), Event()
+            e0.record(s)
+            run()
+            e1.record(s)
+            e1.synchronize()
+            times.append(e0.elapsed_ms(e1))
+            e0.destroy()
+            e1.destroy()
+        lg = logits.numpy()
+        assert np.isfinite(lg).all(), "non-finite logits"
+        out[str(t)] = {"p50_ms": round(float(np.percentile(times, 50)), 3), "min_ms": round(min(times), 3),
+                       "max_ms": round(max(times), 3)}
+    model.close()
+    return {"config": "C5: 36 layers (27 GDN + 9 gated attention), d 2560, d_ff 9216, vocab 151936, "
+                      "3 answers x 8 candidates, random-init", "runs": runs, "tokens": out}
 
 
 def main():
@@ -214,6 +264,8 @@ def main():
         },
         "wall_ms_timed_region": round(wall_ms, 2),
     }
+    if not args.no_forward:
+        out["forward"] = forward_timing(k, args.forward_runs)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:

@@ -50,6 +50,13 @@ class DhGemmPlan(ctypes.Structure):
 
 
 # name -> (restype, argtypes); every symbol include/decide_hip.h declares.
+class DhModelConfig(ctypes.Structure):
+    _fields_ = [("layers", c_uint32), ("vocab", c_uint32), ("max_tokens", c_uint32), ("max_answers", c_uint32),
+                ("max_cand", c_uint32)]
+
+
+DH_FORWARD_NO_PRUNE = 1
+
 PROTOTYPES = {
     "dh_ctx_create": (c_int, [c_uint32, POINTER(c_void_p)]),
     "dh_ctx_destroy": (None, [c_void_p]),
@@ -113,6 +120,14 @@ PROTOTYPES = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32],
     ),
     "dh_fill_normal": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_float, c_float, c_uint32]),
+    "dh_model_create": (c_int, [c_void_p, POINTER(DhModelConfig), POINTER(c_void_p)]),
+    "dh_model_destroy": (None, [c_void_p]),
+    "dh_model_tensor": (c_int, [c_void_p, c_char_p, POINTER(c_void_p), POINTER(c_uint64), POINTER(c_uint32)]),
+    "dh_model_init_random": (c_int, [c_void_p, c_void_p, c_uint64]),
+    "dh_model_forward": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32],
+    ),
 }
 
 _lib = None

@@ -1,0 +1,83 @@
+"""Host mirror of decide's ``Forward`` (crates/decide-engine/src/forward.rs) over the C ABI.
+
+The model owns its weights and activation buffers in device memory (``dh_model_create``), named as in
+decide's ``decide-weights-v1`` index (convert.rs:158-245). ``forward`` enqueues one full-route forward
+(embedding, every layer, the pruned last layer, the candidate head) on a stream; nothing here computes
+anything itself.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .kernels import Arg, Context, _call, addr
+
+DTYPES = {0: np.float16, 1: np.uint16, 2: np.float32}  # bf16 weights are returned as raw bits
+
+
+@dataclass
+class ModelConfig:
+    """decide's model shape parameters that BASELINE varies (config.rs:4-37)."""
+
+    layers: int = 36
+    vocab: int = 151936
+    max_tokens: int = 2307
+    max_answers: int = 16
+    max_cand: int = 62
+
+
+def is_full_attention(layer: int) -> bool:
+    """config.rs:39-41."""
+    return (layer + 1) % 4 == 0
+
+
+class Model:
+    def __init__(self, ctx: Context, cfg: ModelConfig):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.lib = ctx.lib
+        c = _lib.DhModelConfig(cfg.layers, cfg.vocab, cfg.max_tokens, cfg.max_answers, cfg.max_cand)
+        h = ctypes.c_void_p()
+        _call(self.lib.dh_model_create(ctx.handle, ctypes.byref(c), ctypes.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.dh_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor(self, name: str) -> tuple[int, int, type]:
+        """(device address, elements, numpy dtype) of a weight."""
+        ptr, n, dt = ctypes.c_void_p(), ctypes.c_uint64(), ctypes.c_uint32()
+        _call(self.lib.dh_model_tensor(self.handle, name.encode(), ctypes.byref(ptr), ctypes.byref(n),
+                                       ctypes.byref(dt)))
+        return int(ptr.value), int(n.value), DTYPES[dt.value]
+
+    def download(self, name: str) -> np.ndarray:
+        """A weight's values on the host (bf16 as raw uint16 bits)."""
+        from .hip import D2H, check, rt
+
+        ptr, n, dtype = self.tensor(name)
+        out = np.empty(n, dtype=dtype)
+        check(rt().hipMemcpy(out.ctypes.data, ptr, out.nbytes, D2H), "hipMemcpy D2H")
+        return out
+
+    def init_random(self, stream: int, seed: int) -> None:
+        _call(self.lib.dh_model_init_random(self.handle, ctypes.c_void_p(stream), seed))
+
+    def forward(self, stream: int, ids: Arg, t: int, ans_rows: Arg, n_ans: int, cand: Arg, ncand: Arg,
+                logits: Arg, prune: bool = True) -> None:
+        """decide's Forward::logits for the full route, enqueued on ``stream`` (no synchronisation)."""
+        flags = 0 if prune else _lib.DH_FORWARD_NO_PRUNE
+        _call(self.lib.dh_model_forward(self.handle, ctypes.c_void_p(stream), addr(ids), t, addr(ans_rows), n_ans,
+                                        addr(cand), addr(ncand), addr(logits), flags))

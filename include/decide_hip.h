@@ -242,6 +242,50 @@ int dh_attention(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* k
 int dh_fill_normal(dh_ctx* ctx, void* stream, void* out, uint64_t n, uint64_t seed, float mean, float std,
                    uint32_t dtype);
 
+/* ======================================================================
+ * The hybrid decoder forward (decide: Forward, crates/decide-engine/src/
+ * forward.rs): the host that strings the kernels above into decide's layer
+ * order with its buffers and fp16 rounding points, over one stream. It runs
+ * the full route from position 0 as one chunk of all T rows, and prunes the
+ * last layer (full attention) to the answer rows as decide does
+ * (forward.rs:1144-1187). Weights live in device memory the model owns, named
+ * as in decide's decide-weights-v1 index (convert.rs:158-245): "embed" (bf16
+ * [vocab, 2560]), "final_norm", "L{l}.in_norm", "L{l}.w_in", "L{l}.w_out",
+ * "L{l}.post_norm", "L{l}.w_gu", "L{l}.w_down", and per layer kind
+ * "L{l}.conv_w", "L{l}.a_log", "L{l}.dt_bias", "L{l}.gnorm" (Gated-DeltaNet)
+ * or "L{l}.q_norm", "L{l}.k_norm" (attention, layers with (l + 1) % 4 == 0).
+ * ====================================================================== */
+typedef struct dh_model dh_model;
+
+typedef struct dh_model_config {
+  uint32_t layers;       /* decoder layers (decide: 32: 36) */
+  uint32_t vocab;        /* embedding rows (decide: 248,320; BASELINE: 151,936) */
+  uint32_t max_tokens;   /* rows per forward, at most 8192 (decide's MAX_TOKENS) */
+  uint32_t max_answers;  /* answer rows per forward (decide: MAX_ANSWERS 16) */
+  uint32_t max_cand;     /* candidates per answer row (decide: MAX_CANDIDATES 62) */
+} dh_model_config;
+
+/* dh_model_forward flags */
+#define DH_FORWARD_NO_PRUNE 1u /* run the last layer over every row (decide: set_prune(false)) */
+
+/* Allocates the weights and activation buffers on the context's device. */
+int dh_model_create(dh_ctx* ctx, const dh_model_config* cfg, dh_model** out);
+void dh_model_destroy(dh_model* model);
+/* Device address, element count and dtype (0 fp16, 1 bf16, 2 fp32) of a
+ * weight by its decide-weights-v1 name. */
+int dh_model_tensor(const dh_model* model, const char* name, void** ptr, uint64_t* elems, uint32_t* dtype);
+/* Random-initialises every weight on `stream` with dh_fill_normal (BASELINE
+ * config 5: fp16 GEMM weights, bf16 embedding, fp32 small parameters). */
+int dh_model_init_random(dh_model* model, void* stream, uint64_t seed);
+/* One forward over t prompt tokens (device ids [t], each < vocab: the caller
+ * validates ids, as decide's engine does, forward.rs:1494-1537), enqueued on
+ * `stream`. For the n_ans answer rows (device u32 row indices, which are
+ * also their positions) writes logits[r * max_cand + c] for the candidate ids
+ * cand[r * max_cand + c], c < ncand[r] (decide: encode_final_head,
+ * forward.rs:1296-1306). Does not synchronise. */
+int dh_model_forward(dh_model* model, void* stream, const uint32_t* ids, uint32_t t, const uint32_t* ans_rows,
+                     uint32_t n_ans, const uint32_t* cand, const uint32_t* ncand, float* logits, uint32_t flags);
+
 #ifdef __cplusplus
 }
 #endif

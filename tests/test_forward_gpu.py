@@ -1,0 +1,107 @@
+"""The whole hybrid decoder forward on the GPU (dh_model_forward) against the oracle's forward built from
+cpu_ref.rs pieces with decide's rounding points, on a reduced random-init model (same layer shapes, fewer
+layers, small vocab and prompt). Bar: max |Δlogit| <= 0.01.
+The full-size forward (36 layers, 2,307 tokens) is measured by bench.py --forward; here it is checked
+through size-independent properties: finite logits and bitwise determinism across runs."""
+
+import numpy as np
+import pytest
+
+import oracle_forward
+from decide_amd import synth
+from decide_amd.forward import Model, ModelConfig
+from gpu_util import full, sync, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+MAX_LOGIT_DIFF = 0.01  # BASELINE config 5 tolerance
+
+
+def _names(layers):
+    names = ["embed", "final_norm"]
+    for l in range(layers):
+        pre = f"L{l}."
+        names += [pre + n for n in ("in_norm", "w_in", "w_out", "post_norm", "w_gu", "w_down")]
+        if (l + 1) % 4 == 0:
+            names += [pre + "q_norm", pre + "k_norm"]
+        else:
+            names += [pre + n for n in ("conv_w", "a_log", "dt_bias", "gnorm")]
+    return names
+
+
+def _shape(name, n):
+    two_d = {"embed": 2560, "w_in": 2560, "w_gu": 2560, "w_out": None, "w_down": 9216, "conv_w": 4}
+    key = name.split(".")[-1]
+    if key == "w_out":
+        return (2560, n // 2560)
+    if key in two_d:
+        return (n // two_d[key], two_d[key])
+    return (n,)
+
+
+def _request(t, vocab, n_ans, max_cand, seed):
+    ids = synth.uniform_ids(synth.seed_for(seed), t, vocab).astype(np.uint32)
+    ans = np.linspace(t // 3, t - 1, n_ans).astype(np.uint32)
+    cand = synth.uniform_ids(synth.seed_for(seed + 1), n_ans * max_cand, vocab).astype(np.uint32).reshape(n_ans,
+                                                                                                          max_cand)
+    ncand = np.full(n_ans, max_cand, np.uint32)
+    ncand[0] = max_cand - 3  # ragged
+    return ids, ans, cand, ncand
+
+
+def _run(model, kernels, ids, ans, cand, ncand, max_cand, prune):
+    logits = full((len(ans), max_cand), np.float32, np.nan)
+    model.forward(0, (to_dev(ids), 0), len(ids), (to_dev(ans), 0), len(ans), (to_dev(cand), 0), (to_dev(ncand), 0),
+                  (logits, 0), prune=prune)
+    sync()
+    return to_host(logits)
+
+
+@pytest.mark.parametrize("layers,t,prune", [(4, 48, True), (4, 40, False), (8, 70, True)])
+def test_forward_matches_oracle(gpu, kernels, layers, t, prune):
+    cfg = ModelConfig(layers=layers, vocab=1000, max_tokens=96, max_answers=4, max_cand=8)
+    model = Model(kernels.ctx, cfg)
+    kernels.gemm.warm_up(0, max_m=cfg.max_tokens)
+    model.init_random(0, seed=1234 + layers)
+    sync()
+    W = {}
+    for name in _names(layers):
+        W[name] = model.download(name).reshape(_shape(name, model.tensor(name)[1]))
+    ids, ans, cand, ncand = _request(t, cfg.vocab, 3, cfg.max_cand, 300 + layers)
+    got = _run(model, kernels, ids, ans, cand, ncand, cfg.max_cand, prune)
+    want = oracle_forward.forward(W, layers, ids, ans, cand, ncand, cfg.max_cand, prune=prune)
+    written = ~np.isnan(want)
+    assert np.array_equal(~np.isnan(got), written), "entries past ncand must stay untouched"
+    diff = np.abs(got[written] - want[written])
+    assert np.isfinite(got[written]).all()
+    assert diff.max() <= MAX_LOGIT_DIFF, f"max |Δlogit| {diff.max():.4g} (logits up to {np.abs(want[written]).max():.3g})"
+    model.close()
+
+
+def test_forward_pruned_equals_unpruned_within_tolerance(gpu, kernels):
+    """Pruning the last layer to the answer rows changes only which rows are computed (forward.rs:1144-1150)."""
+    cfg = ModelConfig(layers=4, vocab=500, max_tokens=64, max_answers=4, max_cand=6)
+    model = Model(kernels.ctx, cfg)
+    model.init_random(0, seed=77)
+    ids, ans, cand, ncand = _request(50, cfg.vocab, 4, cfg.max_cand, 410)
+    a = _run(model, kernels, ids, ans, cand, ncand, cfg.max_cand, True)
+    b = _run(model, kernels, ids, ans, cand, ncand, cfg.max_cand, False)
+    w = ~np.isnan(a)
+    assert np.abs(a[w] - b[w]).max() <= 1e-3
+    model.close()
+
+
+def test_forward_is_deterministic_and_answer_rows_are_independent(gpu, kernels):
+    cfg = ModelConfig(layers=4, vocab=500, max_tokens=64, max_answers=4, max_cand=6)
+    model = Model(kernels.ctx, cfg)
+    model.init_random(0, seed=78)
+    ids, ans, cand, ncand = _request(60, cfg.vocab, 4, cfg.max_cand, 420)
+    a = _run(model, kernels, ids, ans, cand, ncand, cfg.max_cand, True)
+    b = _run(model, kernels, ids, ans, cand, ncand, cfg.max_cand, True)
+    np.testing.assert_array_equal(a, b)
+    # the pruned layer's GEMMs run at M = answers, so a different count may take a different GEMM plan:
+    # equal within the parity tolerance, not bitwise
+    one = _run(model, kernels, ids, ans[2:3], cand[2:3], ncand[2:3], cfg.max_cand, True)
+    w = ~np.isnan(a[2])
+    assert np.abs(one[0][w] - a[2][w]).max() <= 1e-3
+    model.close()
