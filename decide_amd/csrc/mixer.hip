@@ -8,6 +8,8 @@
 // Model constants are decide's (config.rs:4-31). Every kernel but the
 // recurrence is HBM- or latency-bound; the recurrence is sequential over
 // tokens and bound by its per-token dependency chain.
+#include <type_traits>
+
 #include "dh_kernels.h"
 
 namespace dh {
@@ -112,12 +114,87 @@ hipError_t launch_conv_state_update(const float* p, const float* prev_in, float*
 // state in registers. Per token the two dot products (S·k and S·q) finish
 // with a 16-lane DPP sum, so a token costs ~24 FMAs and 8 DPP adds per lane
 // and no LDS, no barrier. The decay is a running scalar (S = c·S̃, c
-// renormalised into S̃ below 2^-60), the form decide's fast kernel uses.
-// g and β for 64 tokens are computed at once, lane l for token t0 + l, and
-// read back per token with readlane. k, q, v of the next tokens are loaded
-// PF tokens ahead. Grid: (NV heads) × (DV / 16) workgroups of 256 threads.
+// renormalised into S̃ below 2^-60), the form decide's fast kernel uses; c
+// and 1/c depend on the gates only, so they stay off the per-token chain.
+//
+// Memory stays off the chain too. Tokens run in blocks of 64, each block's
+// body fully unrolled: k, q, v of token t + 4 are loaded (index clamped, no
+// branch) while token t computes; g and β of the next block are loaded one
+// block ahead and computed lane-parallel (lane l ↔ token l) at the block
+// start, then read per token with readlane; each row's 64 outputs are kept
+// in registers (lane j holds tokens j, j+16, j+32, j+48) and written once per
+// block. So the only stores, and the only full memory waits, come once per
+// 64 tokens. Grid: (NV heads) × (DV / 16) workgroups of 256 threads.
 constexpr int kDeltaPF = 4;
+constexpr int kDeltaBlock = 64;
 constexpr float kDeltaCMin = 8.673617e-19f;  // 2^-60
+
+namespace {
+struct DeltaLane {
+  const float* __restrict__ q;
+  const float* __restrict__ k;
+  const float* __restrict__ v;
+  uint32_t T, h, hk, dv, j;
+  f4 kr[kDeltaPF][2], qr[kDeltaPF][2];
+  float vr[kDeltaPF];
+  float s[8];
+  float c;
+
+  __device__ __forceinline__ void load(uint32_t t, int slot) {
+    t = min(t, T - 1);
+    const f4* kp = (const f4*)(k + ((size_t)t * NK + hk) * DK + 8 * j);
+    const f4* qp = (const f4*)(q + ((size_t)t * NK + hk) * DK + 8 * j);
+    kr[slot][0] = kp[0];
+    kr[slot][1] = kp[1];
+    qr[slot][0] = qp[0];
+    qr[slot][1] = qp[1];
+    vr[slot] = v[((size_t)t * NV + h) * DV + dv];
+  }
+
+  // One token: consumes ring slot `slot`, refills it with token t + PF; returns o (every lane of the row).
+  __device__ __forceinline__ float step(uint32_t t, int slot, float g, float beta) {
+    const f4 k0 = kr[slot][0], k1 = kr[slot][1], q0 = qr[slot][0], q1 = qr[slot][1];
+    const float vt = vr[slot];
+    load(t + kDeltaPF, slot);
+    float cg = c * g;
+    if (cg < kDeltaCMin) {  // fold the scale into the state (uniform over the wave)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[i] = (s[i] * c) * g;
+      cg = 1.0f;
+    }
+    const float icg = __builtin_amdgcn_rcpf(cg);  // hardware reciprocal, as decide's fast-math division
+    float ka = s[0] * k0[0], kb = s[4] * k1[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+      ka = fmaf(s[i], k0[i], ka);
+      kb = fmaf(s[4 + i], k1[i], kb);
+    }
+    const float kv = row16_sum(ka + kb);
+    const float ds = (vt - cg * kv) * beta * icg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i] = fmaf(k0[i], ds, s[i]);
+      s[4 + i] = fmaf(k1[i], ds, s[4 + i]);
+    }
+    float oa = s[0] * q0[0], ob = s[4] * q1[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+      oa = fmaf(s[i], q0[i], oa);
+      ob = fmaf(s[4 + i], q1[i], ob);
+    }
+    c = cg;
+    return row16_sum(oa + ob) * cg;
+  }
+};
+
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void unroll(Fn&& fn) {
+  if constexpr (B < E) {
+    fn(std::integral_constant<int, B>{});
+    unroll<B + 1, E>(fn);
+  }
+}
+}  // namespace
 
 __global__ __launch_bounds__(256) void gated_delta_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v, const float* __restrict__ a,
@@ -125,94 +202,71 @@ __global__ __launch_bounds__(256) void gated_delta_kernel(const float* __restric
                                                           const float* __restrict__ dt_bias, const float* state_in,
                                                           float* state_out, float* __restrict__ o, uint32_t T,
                                                           uint32_t ldab, uint32_t write_state) {
-  const uint32_t h = blockIdx.x, hk = h >> 1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t dv = blockIdx.y * 16 + wave * 4 + (lane >> 4);
-  const uint32_t j = lane & 15;
-  float s[8];
+  DeltaLane L;
+  L.q = q;
+  L.k = k;
+  L.v = v;
+  L.T = T;
+  L.h = blockIdx.x;
+  L.hk = L.h >> 1;
+  L.dv = blockIdx.y * 16 + wave * 4 + (lane >> 4);
+  L.j = lane & 15;
+  L.c = 1.0f;
   {
-    const f4* src = (const f4*)(state_in + ((size_t)h * DV + dv) * DK + 8 * j);
+    const f4* src = (const f4*)(state_in + ((size_t)L.h * DV + L.dv) * DK + 8 * L.j);
     const f4 s0 = src[0], s1 = src[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      s[i] = s0[i];
-      s[4 + i] = s1[i];
+      L.s[i] = s0[i];
+      L.s[4 + i] = s1[i];
     }
   }
-  const float A = expf(a_log[h]);
-  const float bias = dt_bias[h];
-  // token ring: k, q slices and this row's v, PF tokens ahead
-  f4 kr[kDeltaPF][2], qr[kDeltaPF][2];
-  float vr[kDeltaPF];
-  auto load_tok = [&](uint32_t t, int slot) {
-    if (t < T) {
-      const f4* kp = (const f4*)(k + ((size_t)t * NK + hk) * DK + 8 * j);
-      const f4* qp = (const f4*)(q + ((size_t)t * NK + hk) * DK + 8 * j);
-      kr[slot][0] = kp[0];
-      kr[slot][1] = kp[1];
-      qr[slot][0] = qp[0];
-      qr[slot][1] = qp[1];
-      vr[slot] = v[((size_t)t * NV + h) * DV + dv];
+  const float A = expf(a_log[L.h]);
+  const float bias = dt_bias[L.h];
+  // gate inputs of the first block: lane l ↔ token l (clamped)
+  float av = a[(size_t)min((uint32_t)lane, T - 1) * ldab + L.h];
+  float bv = b[(size_t)min((uint32_t)lane, T - 1) * ldab + L.h];
+#pragma unroll
+  for (int i = 0; i < kDeltaPF; ++i) L.load(i, i);
+
+  for (uint32_t t0 = 0; t0 < T; t0 += kDeltaBlock) {
+    const float gv = expf(-A * softplus_precise(av + bias));
+    const float bt = sigmoid_precise(bv);
+    {  // next block's gate inputs, one block ahead
+      const uint32_t tn = min(t0 + kDeltaBlock + lane, T - 1);
+      av = a[(size_t)tn * ldab + L.h];
+      bv = b[(size_t)tn * ldab + L.h];
     }
-  };
-#pragma unroll
-  for (int i = 0; i < kDeltaPF; ++i) load_tok(i, i);
-  float c = 1.0f;
-  float gv = 0.f, bv = 0.f;
-  for (uint32_t t0 = 0; t0 < T; t0 += kDeltaPF) {
-#pragma unroll
-    for (int u = 0; u < kDeltaPF; ++u) {
-      const uint32_t t = t0 + u;
-      if (t >= T) break;
-      if ((t & 63) == 0) {  // gates of tokens t .. t + 63, lane l → token t + l
-        const uint32_t tl = t + lane;
-        float av = 0.f, bb = 0.f;
-        if (tl < T) {
-          av = a[(size_t)tl * ldab + h];
-          bb = b[(size_t)tl * ldab + h];
+    float keep[4] = {0.f, 0.f, 0.f, 0.f};  // lane j: tokens t0 + j, + 16, + 32, + 48 of its row
+    auto body = [&](auto guard) {
+      unroll<0, kDeltaBlock>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if constexpr (decltype(guard)::value) {
+          if (t0 + u >= T) return;
         }
-        gv = expf(-A * softplus_precise(av + bias));
-        bv = sigmoid_precise(bb);
-      }
-      const float g = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), t & 63));
-      const float beta = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bv), t & 63));
-      const f4 k0 = kr[u][0], k1 = kr[u][1], q0 = qr[u][0], q1 = qr[u][1];
-      const float vt = vr[u];
-      load_tok(t + kDeltaPF, u);
-      float kv = 0.f;
+        const float g = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), u));
+        const float beta = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bt), u));
+        const float ov = L.step(t0 + u, u % kDeltaPF, g, beta);
+        if (L.j == (uint32_t)(u % 16)) keep[u / 16] = ov;
+      });
+    };
+    // full blocks run straight-line code (exact wait counts); only the last block checks T
+    if (t0 + kDeltaBlock <= T)
+      body(std::false_type{});
+    else
+      body(std::true_type{});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kv = fmaf(s[i], k0[i], kv);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kv = fmaf(s[4 + i], k1[i], kv);
-      kv = row16_sum(kv);
-      float cg = c * g;
-      const float delta = (vt - cg * kv) * beta;
-      if (cg < kDeltaCMin) {  // fold the scale back into the state (uniform over the wave)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s[i] = (s[i] * c) * g;
-        cg = 1.0f;
-      }
-      const float ds = delta / cg;
-      float op = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[i] = fmaf(k0[i], ds, s[i]);
-        op = fmaf(s[i], q0[i], op);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[4 + i] = fmaf(k1[i], ds, s[4 + i]);
-        op = fmaf(s[4 + i], q1[i], op);
-      }
-      op = row16_sum(op);
-      if (j == 0) o[((size_t)t * NV + h) * DV + dv] = op * cg;
-      c = cg;
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t t = t0 + 16 * r + L.j;
+      if (t < T) o[((size_t)t * NV + L.h) * DV + L.dv] = keep[r];
     }
   }
   if (write_state) {
-    f4* dst = (f4*)(state_out + ((size_t)h * DV + dv) * DK + 8 * j);
-    dst[0] = f4{s[0] * c, s[1] * c, s[2] * c, s[3] * c};
-    dst[1] = f4{s[4] * c, s[5] * c, s[6] * c, s[7] * c};
+    f4* dst = (f4*)(state_out + ((size_t)L.h * DV + L.dv) * DK + 8 * L.j);
+    const float c = L.c;
+    dst[0] = f4{L.s[0] * c, L.s[1] * c, L.s[2] * c, L.s[3] * c};
+    dst[1] = f4{L.s[4] * c, L.s[5] * c, L.s[6] * c, L.s[7] * c};
   }
 }
 

@@ -81,3 +81,51 @@ class Model:
         flags = 0 if prune else _lib.DH_FORWARD_NO_PRUNE
         _call(self.lib.dh_model_forward(self.handle, ctypes.c_void_p(stream), addr(ids), t, addr(ans_rows), n_ans,
                                         addr(cand), addr(ncand), addr(logits), flags))
+
+
+def main():
+    """Time random-init forwards: python -m decide_amd.forward [--layers 36] [--tokens 2307] [--runs 5]."""
+    import argparse
+    import json
+
+    from . import hip, synth
+    from .hip import DeviceArray, Event, Stream
+    from .kernels import Kernels
+
+    ap = argparse.ArgumentParser(description=main.__doc__)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--vocab", type=int, default=151936)
+    ap.add_argument("--tokens", type=int, default=2307)
+    ap.add_argument("--runs", type=int, default=5)
+    ap.add_argument("--no-prune", action="store_true")
+    args = ap.parse_args()
+    if not hip.available():
+        raise SystemExit("no GPU")
+    k = Kernels()
+    st = Stream()
+    s = st.handle
+    t = args.tokens
+    model = Model(k.ctx, ModelConfig(args.layers, args.vocab, t, 3, 8))
+    model.init_random(s, seed=0xDEC1DE)
+    k.gemm.warm_up(s, max_m=t)
+    ids = DeviceArray.from_numpy(synth.uniform_ids(synth.seed_for(500 + t), t, args.vocab).astype(np.uint32))
+    ans = DeviceArray.from_numpy(np.array([t - 3, t - 2, t - 1], np.uint32))
+    cand = DeviceArray.from_numpy(synth.uniform_ids(synth.seed_for(501 + t), 24, args.vocab).astype(np.uint32))
+    ncand = DeviceArray.from_numpy(np.full(3, 8, np.uint32))
+    logits = DeviceArray((3, 8), np.float32)
+    times = []
+    for i in range(args.runs + 1):
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        model.forward(s, (ids, 0), t, (ans, 0), 3, (cand, 0), (ncand, 0), (logits, 0), prune=not args.no_prune)
+        e1.record(s)
+        e1.synchronize()
+        if i:
+            times.append(e0.elapsed_ms(e1))
+    print(json.dumps({"layers": args.layers, "tokens": t, "runs": args.runs, "p50_ms": float(np.median(times)),
+                      "logits": logits.numpy().round(4).tolist()}), flush=True)
+    model.close()
+
+
+if __name__ == "__main__":
+    main()
