@@ -513,7 +513,11 @@ void gemm_tile_kernel(const TileArgs p) {
   X(10, 3, 3)           \
   X(12, 2, 3)           \
   X(13, 2, 3)           \
-  X(14, 2, 3)
+  X(14, 2, 3)           \
+  X(5, 3, 3)            \
+  X(7, 3, 3)            \
+  X(9, 3, 3)            \
+  X(11, 2, 3)
 
 struct VariantEntry {
   VariantInfo info;
