@@ -134,6 +134,11 @@ struct dh_model {
   }
 };
 
+struct dh_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
 namespace {
 
 #define TRY(expr)                \
@@ -350,6 +355,52 @@ int dh_model_forward(dh_model* m, void* stream, const uint32_t* ids, uint32_t t,
   if (!prune) TRY(dh_gather_rows_f32(m->ctx, s, m->x, ans_rows, m->xs, n_ans, HIDDEN));
   return dh_final_head(m->ctx, s, m->xs, as<float>(m->final_norm->ptr), (const uint16_t*)m->embed->ptr, cand, ncand,
                        logits, n_ans, HIDDEN, m->cfg.max_cand, EPS);
+}
+
+int dh_model_capture(dh_model* m, void* stream, const uint32_t* ids, uint32_t t, const uint32_t* ans_rows,
+                     uint32_t n_ans, const uint32_t* cand, const uint32_t* ncand, float* logits, uint32_t flags,
+                     dh_graph** out) {
+  if (!out) return fail(DH_EINVAL, "model_capture: out is NULL");
+  *out = nullptr;
+  if (!stream) return fail(DH_EINVAL, "model_capture: capture needs a created stream, not the legacy default stream");
+  hipStream_t s = (hipStream_t)stream;
+  // One eager forward first: it sizes every workspace, so nothing allocates while capturing.
+  TRY(dh_model_forward(m, stream, ids, t, ans_rows, n_ans, cand, ncand, logits, flags));
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail(DH_EDEVICE, "model_capture: %s", hipGetErrorString(e));
+  e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return fail(DH_EDEVICE, "model_capture: begin capture: %s", hipGetErrorString(e));
+  const int rc = dh_model_forward(m, stream, ids, t, ans_rows, n_ans, cand, ncand, logits, flags);
+  hipGraph_t g = nullptr;
+  e = hipStreamEndCapture(s, &g);
+  if (rc != DH_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess || !g) return fail(DH_EDEVICE, "model_capture: end capture: %s", hipGetErrorString(e));
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return fail(DH_EDEVICE, "model_capture: instantiate: %s", hipGetErrorString(e));
+  }
+  dh_graph* out_g = new dh_graph();
+  out_g->graph = g;
+  out_g->exec = ex;
+  *out = out_g;
+  return ok();
+}
+
+int dh_graph_launch(dh_graph* g, void* stream) {
+  if (!g || !g->exec) return fail(DH_EINVAL, "graph_launch: null graph");
+  return hip_status(hipGraphLaunch(g->exec, (hipStream_t)stream), "graph_launch");
+}
+
+void dh_graph_destroy(dh_graph* g) {
+  if (!g) return;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
 }
 
 }  // extern "C"

@@ -75,12 +75,43 @@ class Model:
     def init_random(self, stream: int, seed: int) -> None:
         _call(self.lib.dh_model_init_random(self.handle, ctypes.c_void_p(stream), seed))
 
+    def capture(self, stream: int, ids: Arg, t: int, ans_rows: Arg, n_ans: int, cand: Arg, ncand: Arg, logits: Arg,
+                prune: bool = True) -> "Graph":
+        """Run one forward eagerly, then capture the next into a replayable graph (same buffers and sizes)."""
+        flags = 0 if prune else _lib.DH_FORWARD_NO_PRUNE
+        g = ctypes.c_void_p()
+        _call(self.lib.dh_model_capture(self.handle, ctypes.c_void_p(stream), addr(ids), t, addr(ans_rows), n_ans,
+                                        addr(cand), addr(ncand), addr(logits), flags, ctypes.byref(g)))
+        return Graph(self.lib, g)
+
     def forward(self, stream: int, ids: Arg, t: int, ans_rows: Arg, n_ans: int, cand: Arg, ncand: Arg,
                 logits: Arg, prune: bool = True) -> None:
         """decide's Forward::logits for the full route, enqueued on ``stream`` (no synchronisation)."""
         flags = 0 if prune else _lib.DH_FORWARD_NO_PRUNE
         _call(self.lib.dh_model_forward(self.handle, ctypes.c_void_p(stream), addr(ids), t, addr(ans_rows), n_ans,
                                         addr(cand), addr(ncand), addr(logits), flags))
+
+
+class Graph:
+    """A captured whole forward (dh_model_capture): one launch replays every kernel of the forward."""
+
+    def __init__(self, lib, handle):
+        self.lib = lib
+        self.handle = handle
+
+    def launch(self, stream: int) -> None:
+        _call(self.lib.dh_graph_launch(self.handle, ctypes.c_void_p(stream)))
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.dh_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def main():

@@ -286,6 +286,20 @@ int dh_model_init_random(dh_model* model, void* stream, uint64_t seed);
 int dh_model_forward(dh_model* model, void* stream, const uint32_t* ids, uint32_t t, const uint32_t* ans_rows,
                      uint32_t n_ans, const uint32_t* cand, const uint32_t* ncand, float* logits, uint32_t flags);
 
+/* Whole-forward HIP graph (decide has no counterpart: Metal encodes a command
+ * buffer per run; this records the forward's launches once so a serving loop
+ * replays them with one launch). Runs one eager forward on `stream` (so every
+ * workspace is sized before capture), then captures a second into a graph.
+ * Replays read and write the same buffers (ids, answer rows, candidates,
+ * logits) with the same T and answer count; their contents may change between
+ * replays. `stream` must be a created stream, not the legacy default stream. */
+typedef struct dh_graph dh_graph;
+int dh_model_capture(dh_model* model, void* stream, const uint32_t* ids, uint32_t t, const uint32_t* ans_rows,
+                     uint32_t n_ans, const uint32_t* cand, const uint32_t* ncand, float* logits, uint32_t flags,
+                     dh_graph** out);
+int dh_graph_launch(dh_graph* graph, void* stream);
+void dh_graph_destroy(dh_graph* graph);
+
 #ifdef __cplusplus
 }
 #endif

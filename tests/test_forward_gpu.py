@@ -105,3 +105,35 @@ def test_forward_is_deterministic_and_answer_rows_are_independent(gpu, kernels):
     w = ~np.isnan(a[2])
     assert np.abs(one[0][w] - a[2][w]).max() <= 1e-3
     model.close()
+
+
+def test_captured_forward_replays_match_eager(gpu, kernels):
+    """The whole forward captured as one HIP graph: every replay (with eager forwards and new inputs in
+    between) reproduces the eager forward bit for bit."""
+    from decide_amd.hip import Stream
+
+    cfg = ModelConfig(layers=4, vocab=700, max_tokens=64, max_answers=4, max_cand=6)
+    model = Model(kernels.ctx, cfg)
+    st = Stream()
+    s = st.handle
+    model.init_random(s, seed=91)
+    kernels.gemm.warm_up(s, max_m=cfg.max_tokens)
+    ids_a, ans, cand, ncand = _request(56, cfg.vocab, 3, cfg.max_cand, 430)
+    ids_b = _request(56, cfg.vocab, 3, cfg.max_cand, 431)[0]
+    dev = {"ids": to_dev(ids_a), "ans": to_dev(ans), "cand": to_dev(cand), "ncand": to_dev(ncand)}
+    logits = full((3, cfg.max_cand), np.float32, np.nan)
+    graph = model.capture(s, (dev["ids"], 0), 56, (dev["ans"], 0), 3, (dev["cand"], 0), (dev["ncand"], 0),
+                          (logits, 0))
+    st.synchronize()
+    eager_a = _run(model, kernels, ids_a, ans, cand, ncand, cfg.max_cand, True)
+    eager_b = _run(model, kernels, ids_b, ans, cand, ncand, cfg.max_cand, True)
+    for i, (ids, want) in enumerate([(ids_a, eager_a), (ids_b, eager_b), (ids_a, eager_a)]):
+        dev["ids"].copy_from(ids)
+        logits.copy_from(np.full((3, cfg.max_cand), np.nan, np.float32))
+        graph.launch(s)
+        st.synchronize()
+        np.testing.assert_array_equal(to_host(logits), want, err_msg=f"replay {i}")
+        _run(model, kernels, ids_b, ans, cand, ncand, cfg.max_cand, True)  # eager work between replays
+    graph.close()
+    st.destroy()
+    model.close()
