@@ -124,6 +124,8 @@ PROTOTYPES = {
     "dh_model_destroy": (None, [c_void_p]),
     "dh_model_tensor": (c_int, [c_void_p, c_char_p, POINTER(c_void_p), POINTER(c_uint64), POINTER(c_uint32)]),
     "dh_model_init_random": (c_int, [c_void_p, c_void_p, c_uint64]),
+    "dh_model_tensor_name": (c_char_p, [c_void_p, c_uint32]),
+    "dh_model_load": (c_int, [c_void_p, c_char_p]),
     "dh_model_capture": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32,

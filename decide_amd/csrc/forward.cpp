@@ -323,6 +323,11 @@ int dh_model_tensor(const dh_model* m, const char* name, void** ptr, uint64_t* e
   return fail(DH_EINVAL, "model_tensor: no tensor named '%s'", name);
 }
 
+const char* dh_model_tensor_name(const dh_model* m, uint32_t i) {
+  if (!m || i >= m->tensors.size()) return nullptr;
+  return m->tensors[i]->name.c_str();
+}
+
 int dh_model_init_random(dh_model* m, void* stream, uint64_t seed) {
   if (!m) return fail(DH_EINVAL, "model_init_random: null model");
   for (size_t i = 0; i < m->tensors.size(); ++i) {

@@ -72,6 +72,19 @@ class Model:
         check(rt().hipMemcpy(out.ctypes.data, ptr, out.nbytes, D2H), "hipMemcpy D2H")
         return out
 
+    def tensor_names(self) -> list[str]:
+        names, i = [], 0
+        while True:
+            n = self.lib.dh_model_tensor_name(self.handle, i)
+            if n is None:
+                return names
+            names.append(n.decode())
+            i += 1
+
+    def load(self, directory: str) -> None:
+        """Fill every weight from a decide-weights-v1 directory (decide: Weights::open, weights.rs:105-183)."""
+        _call(self.lib.dh_model_load(self.handle, directory.encode()))
+
     def init_random(self, stream: int, seed: int) -> None:
         _call(self.lib.dh_model_init_random(self.handle, ctypes.c_void_p(stream), seed))
 

@@ -274,6 +274,15 @@ void dh_model_destroy(dh_model* model);
 /* Device address, element count and dtype (0 fp16, 1 bf16, 2 fp32) of a
  * weight by its decide-weights-v1 name. */
 int dh_model_tensor(const dh_model* model, const char* name, void** ptr, uint64_t* elems, uint32_t* dtype);
+/* Name of the model's i-th tensor (i from 0 until it returns NULL). */
+const char* dh_model_tensor_name(const dh_model* model, uint32_t i);
+/* Fills every tensor of the model from a decide-weights-v1 directory
+ * (decide: Weights::open, weights.rs:105-183): `decide-index.json` plus the
+ * blobs it lists, tensors at 16 KiB-aligned offsets. Checks decide's format
+ * tag, dtypes, alignment and bounds, and that each tensor has the dtype and
+ * element count the model holds. Blobs are memory-mapped and each tensor is
+ * copied once into device memory. Synchronous. */
+int dh_model_load(dh_model* model, const char* dir);
 /* Random-initialises every weight on `stream` with dh_fill_normal (BASELINE
  * config 5: fp16 GEMM weights, bf16 embedding, fp32 small parameters). */
 int dh_model_init_random(dh_model* model, void* stream, uint64_t seed);
