@@ -20,6 +20,7 @@ DH_ENOMEM = 3
 DH_EDEVICE = 4
 
 DH_GEMM_REFERENCE = 1
+DH_DELTA_CHUNKED = 2
 
 
 class DhGemmMember(ctypes.Structure):

@@ -48,6 +48,24 @@ void mark(dh_ctx* c, int kid) { c->used.fetch_or(1ull << kid, std::memory_order_
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+int ensure_aux(dh_ctx* c, uint64_t bytes) {
+  std::lock_guard<std::mutex> g(c->ws_lock);
+  if (bytes <= c->aux_bytes) return DH_OK;
+  if (c->aux) {
+    hipError_t e = hipFree(c->aux);
+    c->aux = nullptr;
+    c->aux_bytes = 0;
+    if (e != hipSuccess) return fail(DH_EDEVICE, "forward workspace: hipFree: %s", hipGetErrorString(e));
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess)
+    return fail(DH_ENOMEM, "forward workspace of %llu bytes: %s", (unsigned long long)bytes, hipGetErrorString(e));
+  c->aux = (float*)p;
+  c->aux_bytes = bytes;
+  return DH_OK;
+}
+
 }  // namespace dh_api
 
 using namespace dh_api;
@@ -151,7 +169,8 @@ const char* dh_version(void) { return "decide-hip 0.1.0 (gfx950, fp16 MFMA 16x16
 int dh_ctx_create(uint32_t flags, dh_ctx** out) {
   if (!out) return fail(DH_EINVAL, "dh_ctx_create: out is NULL");
   *out = nullptr;
-  if (flags & ~DH_GEMM_REFERENCE) return fail(DH_EINVAL, "dh_ctx_create: unknown flags 0x%x", flags);
+  if (flags & ~(DH_GEMM_REFERENCE | DH_DELTA_CHUNKED))
+    return fail(DH_EINVAL, "dh_ctx_create: unknown flags 0x%x", flags);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(DH_EDEVICE, "dh_ctx_create: no HIP device: %s", hipGetErrorString(e));
@@ -170,6 +189,7 @@ int dh_ctx_create(uint32_t flags, dh_ctx** out) {
 void dh_ctx_destroy(dh_ctx* ctx) {
   if (!ctx) return;
   if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->aux) (void)hipFree(ctx->aux);
   delete ctx;
 }
 
@@ -290,6 +310,10 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
     }
   if (need) {
     int rc = ensure_ws(ctx, need);
+    if (rc != DH_OK) return rc;
+  }
+  if (ctx->flags & DH_DELTA_CHUNKED) {  // the chunked recurrence's workspace for max_m tokens
+    int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(std::max(1u, max_m)) * sizeof(float));
     if (rc != DH_OK) return rc;
   }
   // One tiny launch of every tile variant (M = 16, N = bn, K = 64) into scratch.

@@ -17,6 +17,8 @@ struct dh_ctx {
   float* ws = nullptr;
   uint64_t ws_bytes = 0;
   uint64_t ws_cap = 512ull << 20;  // split-K workspace ceiling
+  float* aux = nullptr;            // forward-kernel workspace (the chunked recurrence's per-chunk matrices)
+  uint64_t aux_bytes = 0;
   int forced_variant = -1;
   uint32_t forced_splits = 0;
   std::atomic<uint64_t> used{0};  // bit per distinct kernel launched
@@ -27,7 +29,8 @@ namespace dh_api {
 // Kernel ids for dh_variants_loaded beyond the tile menu (ids < 48).
 enum : int {
   kKidReduce = 48, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
-  kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny
+  kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny,
+  kKidDeltaChunk
 };
 
 // Records `fmt` as the thread's last error and returns `code`.
@@ -39,5 +42,7 @@ int hip_status(hipError_t e, const char* what);
 // Records that kernel `kid` has been launched through this context.
 void mark(dh_ctx* c, int kid);
 bool aligned(const void* p, uintptr_t a);
+// Grows the context's forward-kernel workspace to at least `bytes` (hipMalloc only when it grows).
+int ensure_aux(dh_ctx* c, uint64_t bytes);
 
 }  // namespace dh_api

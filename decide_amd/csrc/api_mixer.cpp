@@ -65,10 +65,19 @@ int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, co
   if (misaligned(q, 16) || misaligned(k, 16) || misaligned(state_in, 16) || misaligned(state_out, 16))
     return fail(DH_EINVAL, "delta: q, k and the states must be 16-byte aligned");
   if (!ctx) return fail(DH_EINVAL, "delta: null context");
-  mark(ctx, kKidDelta);
-  return hip_status(dh::launch_gated_delta(q, k, v, a, b, a_log, dt_bias, state_in, state_out, o, t, ldab,
-                                           write_state != 0, (hipStream_t)stream),
-                    "gated_delta");
+  if (!(ctx->flags & DH_DELTA_CHUNKED)) {
+    mark(ctx, kKidDelta);
+    return hip_status(dh::launch_gated_delta(q, k, v, a, b, a_log, dt_bias, state_in, state_out, o, t, ldab,
+                                             write_state != 0, (hipStream_t)stream),
+                      "gated_delta");
+  }
+  // allocates only when T exceeds what dh_warm_up sized the workspace for
+  const int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(t) * sizeof(float));
+  if (rc != DH_OK) return rc;
+  mark(ctx, kKidDeltaChunk);
+  return hip_status(dh::launch_gated_delta_chunked(q, k, v, a, b, a_log, dt_bias, state_in, state_out, o, ctx->aux, t,
+                                                   ldab, write_state != 0, (hipStream_t)stream),
+                    "gated_delta (chunked)");
 }
 
 int dh_gated_rmsnorm_silu(dh_ctx* ctx, void* stream, const float* o, const float* z, const float* w, uint16_t* y,

@@ -75,6 +75,12 @@ hipError_t launch_conv_state_update(const float* p, const float* prev_in, float*
 hipError_t launch_gated_delta(const float* q, const float* k, const float* v, const float* a, const float* b,
                               const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
                               float* o, uint32_t t, uint32_t ldab, bool write_state, hipStream_t s);
+// The chunked recurrence (delta_chunk.hip): `ws` holds delta_chunk_ws_floats(t) floats.
+size_t delta_chunk_ws_floats(uint32_t t);
+hipError_t launch_gated_delta_chunked(const float* q, const float* k, const float* v, const float* a, const float* b,
+                                      const float* a_log, const float* dt_bias, const float* state_in,
+                                      float* state_out, float* o, float* ws, uint32_t t, uint32_t ldab,
+                                      bool write_state, hipStream_t s);
 hipError_t launch_gated_rmsnorm_silu(const float* o, const float* z, const float* w, _Float16* y, uint32_t t,
                                      uint32_t ldz, hipStream_t s);
 hipError_t launch_q_norm_rope(const float* pq, const float* qw, const float* inv_freq, const uint32_t* qpos,

@@ -64,10 +64,12 @@ def _call(rc: int) -> None:
 class Context:
     """One library context (the analog of the pipelines ``Kernels::new`` builds)."""
 
-    def __init__(self, imp: GemmImpl = GemmImpl.Fast):
+    def __init__(self, imp: GemmImpl = GemmImpl.Fast, delta_chunked: bool = False):
         lib = _lib.load()
         h = ctypes.c_void_p()
         flags = _lib.DH_GEMM_REFERENCE if imp == GemmImpl.Baseline else 0
+        if delta_chunked:  # the recurrence's other implementation (decide's DECIDE_DELTA, kernels/delta.rs:36-49)
+            flags |= _lib.DH_DELTA_CHUNKED
         _lib.check(lib.dh_ctx_create(flags, ctypes.byref(h)))
         self.handle = h
         self.imp = imp
@@ -292,8 +294,8 @@ def fill_normal_f16(ctx: Context, stream: int, out: Arg, n: int, seed: int, std:
 class Kernels:
     """decide's ``Kernels`` registry (kernels/mod.rs:40-67): the GEMM path and the forward kernels beside it."""
 
-    def __init__(self, imp: GemmImpl = GemmImpl.Fast):
-        self.ctx = Context(imp)
+    def __init__(self, imp: GemmImpl = GemmImpl.Fast, delta_chunked: bool = False):
+        self.ctx = Context(imp, delta_chunked)
         self.gemm = Gemm(self.ctx)
         self.head = Head(self.ctx)
         self.norm = Norm(self.ctx)

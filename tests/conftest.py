@@ -47,3 +47,13 @@ def kernels_ref(gpu):
 def stream(gpu):
     """The legacy default stream (0): synchronous copies order against it."""
     return 0
+
+
+@pytest.fixture(scope="session")
+def kernels_delta_chunked(gpu):
+    """A context whose gated delta runs the chunked recurrence."""
+    from decide_amd.kernels import Kernels
+
+    k = Kernels(delta_chunked=True)
+    yield k
+    k.ctx.close()

@@ -240,3 +240,44 @@ def test_embed_widens_bf16_bitwise():
     out = orc.embed_bf16(ids, table)
     want = (table[ids].astype(np.uint32) << 16).view(np.float32)
     np.testing.assert_array_equal(out.view(np.uint32), want.view(np.uint32))
+
+
+def chunked_delta64(q, k, v, a, b, a_log, dt_bias, s0, C=64):
+    """The chunked (WY-form) gated delta rule in float64, the formulation the GPU kernel uses:
+    per chunk, A_ij = β_i (γ_i/γ_j) k_i·k_j (i > j), T = (I + A)⁻¹, W = T diag(βγ) K, U = T diag(β) V,
+    V' = U − W Sᵀ, O = diag(γ) Q Sᵀ + (Q Kᵀ ⊙ Γ) V' (Γ_ij = γ_i/γ_j, i ≥ j), S ← γ_C S + V'ᵀ diag(γ_C/γ) K."""
+    t = q.shape[0]
+    S = s0.astype(np.float64).copy()
+    o = np.zeros((t, NV, DV))
+    A_ = np.exp(a_log.astype(np.float64))
+    for c0 in range(0, t, C):
+        n = min(C, t - c0)
+        for h in range(NV):
+            hk = h // 2
+            x = a[c0:c0 + n, h].astype(np.float64) + dt_bias[h]
+            lam = -A_[h] * np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20))))
+            Lg = np.cumsum(lam)
+            beta = sig64(b[c0:c0 + n, h])
+            K = k[c0:c0 + n, hk].astype(np.float64)
+            Q = q[c0:c0 + n, hk].astype(np.float64)
+            V = v[c0:c0 + n, h].astype(np.float64)
+            R = np.exp(Lg[:, None] - Lg[None, :])
+            Am = np.tril(beta[:, None] * R * (K @ K.T), -1)
+            T = np.linalg.inv(np.eye(n) + Am)
+            W = T @ (beta[:, None] * np.exp(Lg)[:, None] * K)
+            U = T @ (beta[:, None] * V)
+            Vp = U - W @ S[h].T
+            M = np.tril(R * (Q @ K.T))
+            o[c0:c0 + n, h] = np.exp(Lg)[:, None] * (Q @ S[h].T) + M @ Vp
+            S[h] = np.exp(Lg[-1]) * S[h] + Vp.T @ (np.exp(Lg[-1] - Lg)[:, None] * K)
+    return o, S
+
+
+@pytest.mark.parametrize("t", [1, 5, 64, 150])
+def test_chunked_delta_formulation_equals_the_recurrence(t):
+    """Pins the chunked form the GPU's chunk kernels implement against the oracle's token-by-token rule."""
+    q, k, v, a, b, a_log, dt_bias, st = _delta_inputs(t, 60, state_std=0.05)
+    o_ref, s_ref = orc.gated_delta(q, k, v, a, b, a_log, dt_bias, st, t)
+    o, s = chunked_delta64(q, k, v, a, b, a_log, dt_bias, st)
+    np.testing.assert_allclose(o, o_ref, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(s, s_ref, rtol=1e-4, atol=1e-7)
