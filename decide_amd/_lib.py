@@ -56,7 +56,17 @@ class DhModelConfig(ctypes.Structure):
                 ("max_cand", c_uint32)]
 
 
+class DhAnswer(ctypes.Structure):
+    """``dh_answer`` (include/decide_hip.h): one answer row and its host candidate ids."""
+
+    _fields_ = [("row", c_uint32), ("ncand", c_uint32), ("cand", POINTER(c_uint32))]
+
+
 DH_FORWARD_NO_PRUNE = 1
+DH_LOGITS_FULL = 1
+DH_ROUTE_SNAPSHOT = 0
+DH_ROUTE_FULL = 1
+DH_ROUTE_STATE_CACHE = 2
 
 PROTOTYPES = {
     "dh_ctx_create": (c_int, [c_uint32, POINTER(c_void_p)]),
@@ -138,6 +148,23 @@ PROTOTYPES = {
         c_int,
         [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32],
     ),
+    "dh_model_logits": (
+        c_int, [c_void_p, c_void_p, POINTER(c_uint32), c_uint32, POINTER(DhAnswer), c_uint32, POINTER(c_float), c_uint32]),
+    "dh_model_build_snapshot": (c_int, [c_void_p, c_void_p, POINTER(c_uint32), c_uint32]),
+    "dh_model_prefix_len": (c_int, [c_void_p, POINTER(c_uint32), POINTER(c_int)]),
+    "dh_model_last_route": (c_int, [c_void_p, POINTER(ctypes.c_int32), POINTER(ctypes.c_int64)]),
+    "dh_model_set_chunk": (c_int, [c_void_p, c_uint32]),
+    "dh_model_chunk": (c_uint32, [c_void_p]),
+    "dh_model_set_pruning": (None, [c_void_p, c_int]),
+    "dh_model_pruning": (c_int, [c_void_p]),
+    "dh_model_set_state_cache": (c_int, [c_void_p, c_uint32]),
+    "dh_model_state_cache_capacity": (c_uint32, [c_void_p]),
+    "dh_model_forget_states": (None, [c_void_p]),
+    "dh_model_cached_states": (c_uint32, [c_void_p, POINTER(c_uint32), c_uint32]),
+    "dh_model_set_state_marker": (c_int, [c_void_p, POINTER(c_uint32), c_uint32]),
+    "dh_state_boundary": (
+        c_int, [POINTER(c_uint32), c_uint32, c_uint32, POINTER(c_uint32), c_uint32, c_uint32, POINTER(c_uint32),
+                POINTER(c_int)]),
 }
 
 _lib = None

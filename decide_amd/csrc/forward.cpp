@@ -1,24 +1,24 @@
 // The hybrid decoder forward over the C ABI: decide's Forward
-// (crates/decide-engine/src/forward.rs) restated for one MI355X.
+// (crates/decide-engine/src/forward.rs) restated for one MI355X. This file
+// holds the weights, the buffers and one chunk's work; session.cpp runs
+// requests as chunks against the prefix snapshot and the state cache.
 //
-// decide runs a request as chunks of at most CHUNK = 512 rows (config.rs:36)
-// against a prefix snapshot and a state cache. This host keeps decide's layer
-// order, buffers, fp16 rounding points and last-layer pruning
-// (forward.rs:1125-1310), and runs the full route from position 0 as ONE
-// chunk of all T rows: with 288 GB of HBM every activation of a 2,307-token
-// prompt fits many times over, and one chunk gives every GEMM its largest M.
+// decide's layer order, buffers, fp16 rounding points and last-layer pruning
+// (forward.rs:1118-1310) are kept. Chunks default to the whole span (up to
+// max_tokens rows): with 288 GB of HBM every activation of a long prompt fits
+// many times over, and one chunk gives every GEMM its largest M.
 //
-// Layer l (decide: encode_layer, forward.rs:1197-1268):
+// Layer l of a chunk (decide: encode_layer, forward.rs:1189-1268):
 //   h = rmsnorm(x, in_norm) fp16
 //   Gated-DeltaNet (l + 1) % 4 != 0:
 //     p = h·w_inᵀ (qkv | z | b | a, fp32) → conv+SiLU+L2 → q, k, v
-//     o = gated_delta(q, k, v, a, b) from zero state → g = gnorm(o, z) fp16
+//     o = gated_delta(q, k, v, a, b) from the carried state → g = gnorm(o, z) fp16
 //   attention:
 //     p = h·w_inᵀ (q | gate | k | v) → qo = norm+RoPE(q) fp16; kc, vc caches
-//     g = attention(qo, kc, vc, gate) fp16
+//     at the chunk's positions; g = attention(qo, kc, vc, gate) fp16
 //   x += g·w_outᵀ;  h = rmsnorm(x, post_norm);  x += SwiGLU(h·w_guᵀ)·w_downᵀ
 // The last layer (attention) is pruned to the answer rows when asked, as
-// decide does (encode_last_layer_pruned, forward.rs:1144-1187): K/V for
+// decide does (encode_last_layer_pruned, forward.rs:1133-1187): K/V for
 // every row, everything else for the answer rows only; then the candidate
 // head (final_head) on the answer rows.
 #include <hip/hip_runtime.h>
@@ -30,109 +30,34 @@
 #include <vector>
 
 #include "../../include/decide_hip.h"
-#include "api_internal.h"
+#include "model_internal.h"
 
 using namespace dh_api;
+using namespace dh_model_impl;
 
-namespace {
-
-constexpr uint32_t HIDDEN = 2560, NK = 16, DK = 128, NV = 32, DV = 128;
-constexpr uint32_t KEY_DIM = NK * DK, VALUE_DIM = NV * DV, CONV_DIM = 2 * KEY_DIM + VALUE_DIM, CONV_K = 4;
-constexpr uint32_t LIN_IN_N = CONV_DIM + VALUE_DIM + 2 * NV, LIN_Z = CONV_DIM, LIN_B = CONV_DIM + VALUE_DIM,
-                   LIN_A = LIN_B + NV;
-constexpr uint32_t NQ = 16, NKV = 4, HEAD_DIM = 256, Q_DIM = NQ * HEAD_DIM, KV_DIM = NKV * HEAD_DIM;
-constexpr uint32_t ATT_IN_N = 2 * Q_DIM + 2 * KV_DIM, ATT_K = 2 * Q_DIM, ATT_V = 2 * Q_DIM + KV_DIM;
-constexpr uint32_t INTER = 9216, MLP_IN_N = 2 * INTER, ROT_HALF = 32;
-constexpr float EPS = 1e-6f;
-constexpr uint32_t kCacheRowsMax = 8192;  // decide's MAX_TOKENS: the K/V cache height
-
-bool is_full_attention(uint32_t l) { return (l + 1) % 4 == 0; }  // config.rs:39-41
-
-enum DType : uint32_t { F16 = 0, BF16 = 1, F32 = 2 };
-
-struct Tensor {
-  std::string name;
-  void* ptr = nullptr;
-  uint64_t elems = 0;
-  DType dtype = F16;
-  float mean = 0.f, std = 0.f;  // random-init distribution
-  uint64_t bytes() const { return elems * (dtype == F32 ? 4 : 2); }
-};
-
-struct Layer {
-  bool attn = false;
-  uint32_t att_index = 0;  // index into the K/V caches
-  Tensor* in_norm = nullptr;
-  Tensor* post_norm = nullptr;
-  Tensor* w_in = nullptr;
-  Tensor* w_out = nullptr;
-  Tensor* w_gu = nullptr;
-  Tensor* w_down = nullptr;
-  Tensor* conv_w = nullptr;
-  Tensor* a_log = nullptr;
-  Tensor* dt_bias = nullptr;
-  Tensor* gnorm = nullptr;
-  Tensor* q_norm = nullptr;
-  Tensor* k_norm = nullptr;
-};
-
-template <typename T>
-T* as(void* p) {
-  return (T*)p;
+dh_model::~dh_model() {
+  for (void* a : allocs) (void)hipFree(a);
+  for (Tensor* t : tensors) delete t;
 }
 
-}  // namespace
+void* dh_model::alloc(uint64_t bytes) {
+  void* ptr = nullptr;
+  if (hipMalloc(&ptr, bytes ? bytes : 16) != hipSuccess) return nullptr;
+  allocs.push_back(ptr);
+  return ptr;
+}
 
-struct dh_model {
-  dh_ctx* ctx = nullptr;
-  dh_model_config cfg{};
-  std::vector<Tensor*> tensors;  // owned
-  Tensor* embed = nullptr;
-  Tensor* final_norm = nullptr;
-  std::vector<Layer> layers;
-  // activations (decide: Buffers, forward.rs:124-180), sized for cfg.max_tokens rows
-  float* x = nullptr;
-  _Float16* h = nullptr;
-  float* p = nullptr;
-  float* q = nullptr;
-  float* k = nullptr;
-  float* v = nullptr;
-  float* o = nullptr;
-  _Float16* g = nullptr;
-  _Float16* mlp = nullptr;
-  _Float16* qo = nullptr;
-  std::vector<_Float16*> kc, vc;
-  float* zero_state = nullptr;
-  float* zero_conv = nullptr;
-  uint32_t* iota = nullptr;
-  float* inv_freq = nullptr;
-  float* xs = nullptr;
-  _Float16* hs = nullptr;
-  float* ps = nullptr;
-  std::vector<void*> allocs;
-
-  ~dh_model() {
-    for (void* a : allocs) (void)hipFree(a);
-    for (Tensor* t : tensors) delete t;
-  }
-  void* alloc(uint64_t bytes) {
-    void* ptr = nullptr;
-    if (hipMalloc(&ptr, bytes ? bytes : 16) != hipSuccess) return nullptr;
-    allocs.push_back(ptr);
-    return ptr;
-  }
-  Tensor* add(const std::string& name, uint64_t elems, DType dt, float mean, float std) {
-    Tensor* t = new Tensor();
-    t->name = name;
-    t->elems = elems;
-    t->dtype = dt;
-    t->mean = mean;
-    t->std = std;
-    t->ptr = alloc(t->bytes());
-    tensors.push_back(t);
-    return t->ptr ? t : nullptr;
-  }
-};
+Tensor* dh_model::add(const std::string& name, uint64_t elems, DType dt, float mean, float std) {
+  Tensor* t = new Tensor();
+  t->name = name;
+  t->elems = elems;
+  t->dtype = dt;
+  t->mean = mean;
+  t->std = std;
+  t->ptr = alloc(t->bytes());
+  tensors.push_back(t);
+  return t->ptr ? t : nullptr;
+}
 
 struct dh_graph {
   hipGraph_t graph = nullptr;
@@ -146,6 +71,11 @@ namespace {
     const int rc_ = (expr);      \
     if (rc_ != DH_OK) return rc_; \
   } while (0)
+
+template <typename T>
+T* as(void* p) {
+  return (T*)p;
+}
 
 // h = rmsnorm(x rows) fp16 with (1 + w).
 int norm(dh_model* m, void* s, const float* x, const Tensor* w, _Float16* y, uint32_t rows) {
@@ -164,49 +94,129 @@ int mlp(dh_model* m, void* s, const Layer& L, float* x, _Float16* h, uint32_t ro
   return gemm(m, s, m->mlp, INTER, L.w_down->ptr, INTER, x, HIDDEN, rows, HIDDEN, INTER, DH_EPI_ADD_F32);
 }
 
-int layer_full(dh_model* m, void* s, const Layer& L, uint32_t t) {
-  TRY(norm(m, s, m->x, L.in_norm, m->h, t));
-  if (!L.attn) {
-    TRY(gemm(m, s, m->h, HIDDEN, L.w_in->ptr, HIDDEN, m->p, LIN_IN_N, t, LIN_IN_N, HIDDEN, DH_EPI_STORE_F32));
-    TRY(dh_conv_silu_l2(m->ctx, s, m->p, m->zero_conv, as<float>(L.conv_w->ptr), m->q, m->k, m->v, t, LIN_IN_N));
-    TRY(dh_gated_delta(m->ctx, s, m->q, m->k, m->v, m->p + LIN_A, m->p + LIN_B, as<float>(L.a_log->ptr),
-                       as<float>(L.dt_bias->ptr), m->zero_state, nullptr, m->o, t, LIN_IN_N, 0));
-    TRY(dh_gated_rmsnorm_silu(m->ctx, s, m->o, m->p + LIN_Z, as<float>(L.gnorm->ptr), (uint16_t*)m->g, t, LIN_IN_N));
-  } else {
-    TRY(gemm(m, s, m->h, HIDDEN, L.w_in->ptr, HIDDEN, m->p, ATT_IN_N, t, ATT_IN_N, HIDDEN, DH_EPI_STORE_F32));
-    TRY(dh_q_norm_rope(m->ctx, s, m->p, as<float>(L.q_norm->ptr), m->inv_freq, m->iota, (uint16_t*)m->qo, t,
-                       ATT_IN_N));
-    TRY(dh_kv_norm_rope(m->ctx, s, m->p, as<float>(L.k_norm->ptr), m->inv_freq, (uint16_t*)m->kc[L.att_index],
-                        (uint16_t*)m->vc[L.att_index], t, ATT_IN_N, ATT_K, ATT_V, 0));
-    TRY(dh_attention(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
-                     (const uint16_t*)m->vc[L.att_index], m->p, m->iota, (uint16_t*)m->g, t, ATT_IN_N));
+// The (conv, recurrent) state chunk 0 of a run reads for linear layer i (decide: source, forward.rs:1036-1046).
+void source_of(dh_model* m, Source src, uint32_t i, const float** conv, const float** state) {
+  switch (src.kind) {
+    case SourceKind::Zero:
+      *conv = m->zero_conv;
+      *state = m->zero_state;
+      break;
+    case SourceKind::Snapshot:
+      *conv = m->snapshot.conv[i].as<float>();
+      *state = m->snapshot.state[i].as<float>();
+      break;
+    case SourceKind::State:
+      *conv = m->states[src.entry].conv[i].as<float>();
+      *state = m->states[src.entry].state[i].as<float>();
+      break;
   }
-  TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, m->x, HIDDEN, t, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
-  return mlp(m, s, L, m->x, m->h, t);
 }
 
-// decide: encode_last_layer_pruned (forward.rs:1144-1187).
-int layer_pruned(dh_model* m, void* s, const Layer& L, uint32_t t, const uint32_t* ans_rows, uint32_t n) {
+// The recurrence over chunk rows from..to, from state_in to state_out (forward.rs:1208-1216).
+int delta(dh_model* m, void* s, const Layer& L, uint32_t from, uint32_t to, const float* state_in, float* state_out,
+          bool write) {
+  const float* pa = m->p + (size_t)from * LIN_IN_N;
+  return dh_gated_delta(m->ctx, s, m->q + (size_t)from * KEY_DIM, m->k + (size_t)from * KEY_DIM,
+                        m->v + (size_t)from * VALUE_DIM, pa + LIN_A, pa + LIN_B, as<float>(L.a_log->ptr),
+                        as<float>(L.dt_bias->ptr), state_in, state_out, m->o + (size_t)from * VALUE_DIM, to - from,
+                        LIN_IN_N, write ? 1u : 0u);
+}
+
+// Layer L over every row of the chunk (decide: encode_layer, forward.rs:1189-1268).
+int layer_full(dh_model* m, void* s, const Layer& L, const Chunk& ch, Source src, const StateEntry* entry) {
+  const uint32_t rows = ch.rows;
+  TRY(norm(m, s, m->x, L.in_norm, m->h, rows));
+  if (!L.attn) {
+    const uint32_t i = L.lin_index;
+    TRY(gemm(m, s, m->h, HIDDEN, L.w_in->ptr, HIDDEN, m->p, LIN_IN_N, rows, LIN_IN_N, HIDDEN, DH_EPI_STORE_F32));
+    const float* conv_in = m->conv[i];
+    const float* state_in = m->state[i];
+    if (ch.first) source_of(m, src, i, &conv_in, &state_in);
+    TRY(dh_conv_silu_l2(m->ctx, s, m->p, conv_in, as<float>(L.conv_w->ptr), m->q, m->k, m->v, rows, LIN_IN_N));
+    const bool capture = entry && ch.capture;
+    // the capture's update reads conv_in before the in-place update below may overwrite it
+    if (capture) TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, entry->conv[i].as<float>(), ch.capture, LIN_IN_N));
+    if (ch.keep_state) TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, m->conv[i], rows, LIN_IN_N));
+    if (capture) {
+      // split at the end of the state: the state there goes to the entry, and the
+      // rest of the chunk continues from it (fp32 through memory, so exactly)
+      float* at = entry->state[i].as<float>();
+      TRY(delta(m, s, L, 0, ch.capture, state_in, at, true));
+      if (ch.capture < rows)
+        TRY(delta(m, s, L, ch.capture, rows, at, m->state[i], ch.keep_state));
+      else if (ch.keep_state)
+        TRY(hip_status(hipMemcpyAsync(m->state[i], at, kStateBytes, hipMemcpyDeviceToDevice, (hipStream_t)s),
+                       "state copy"));
+    } else {
+      TRY(delta(m, s, L, 0, rows, state_in, m->state[i], ch.keep_state));
+    }
+    TRY(dh_gated_rmsnorm_silu(m->ctx, s, m->o, m->p + LIN_Z, as<float>(L.gnorm->ptr), (uint16_t*)m->g, rows,
+                              LIN_IN_N));
+  } else {
+    const uint32_t* qpos = m->iota + ch.pos0;
+    TRY(gemm(m, s, m->h, HIDDEN, L.w_in->ptr, HIDDEN, m->p, ATT_IN_N, rows, ATT_IN_N, HIDDEN, DH_EPI_STORE_F32));
+    TRY(dh_q_norm_rope(m->ctx, s, m->p, as<float>(L.q_norm->ptr), m->inv_freq, qpos, (uint16_t*)m->qo, rows,
+                       ATT_IN_N));
+    TRY(dh_kv_norm_rope(m->ctx, s, m->p, as<float>(L.k_norm->ptr), m->inv_freq, (uint16_t*)m->kc[L.att_index],
+                        (uint16_t*)m->vc[L.att_index], rows, ATT_IN_N, ATT_K, ATT_V, ch.pos0));
+    TRY(dh_attention(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
+                     (const uint16_t*)m->vc[L.att_index], m->p, qpos, (uint16_t*)m->g, rows, ATT_IN_N));
+  }
+  TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, m->x, HIDDEN, rows, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
+  return mlp(m, s, L, m->x, m->h, rows);
+}
+
+// Final norm + candidate logits of the chunk's answers from xs (decide: encode_final_head, forward.rs:1296-1306).
+int final_head(dh_model* m, void* s, const RunArgs& r, const Chunk& ch) {
+  const uint32_t a0 = ch.a0, mc = m->cfg.max_cand;
+  return dh_final_head(m->ctx, s, m->xs + (size_t)a0 * HIDDEN, as<float>(m->final_norm->ptr),
+                       (const uint16_t*)m->embed->ptr, r.cand + (size_t)a0 * mc, r.ncand + a0,
+                       r.logits + (size_t)a0 * mc, ch.n, HIDDEN, mc, EPS);
+}
+
+// The last layer (full attention) pruned to the chunk's answer rows
+// (decide: encode_last_layer_pruned, forward.rs:1133-1187).
+int layer_pruned(dh_model* m, void* s, const Layer& L, const RunArgs& r, const Chunk& ch) {
   const _Float16* w_in = as<_Float16>(L.w_in->ptr);
-  TRY(norm(m, s, m->x, L.in_norm, m->h, t));
+  TRY(norm(m, s, m->x, L.in_norm, m->h, ch.rows));
   // rows ATT_K.. of w_in are k|v
-  TRY(gemm(m, s, m->h, HIDDEN, w_in + (size_t)ATT_K * HIDDEN, HIDDEN, m->p, 2 * KV_DIM, t, 2 * KV_DIM, HIDDEN,
+  TRY(gemm(m, s, m->h, HIDDEN, w_in + (size_t)ATT_K * HIDDEN, HIDDEN, m->p, 2 * KV_DIM, ch.rows, 2 * KV_DIM, HIDDEN,
            DH_EPI_STORE_F32));
   TRY(dh_kv_norm_rope(m->ctx, s, m->p, as<float>(L.k_norm->ptr), m->inv_freq, (uint16_t*)m->kc[L.att_index],
-                      (uint16_t*)m->vc[L.att_index], t, 2 * KV_DIM, 0, KV_DIM, 0));
-  if (n == 0) return ok();
-  TRY(dh_gather_rows_f16(m->ctx, s, (const uint16_t*)m->h, ans_rows, (uint16_t*)m->hs, n, HIDDEN));
+                      (uint16_t*)m->vc[L.att_index], ch.rows, 2 * KV_DIM, 0, KV_DIM, ch.pos0));
+  if (ch.n == 0) return ok();
+  const uint32_t n = ch.n, a0 = ch.a0;
+  const uint32_t* rowmap = r.ans_rows + a0;
+  const uint32_t* qpos = r.ans_pos + a0;
+  _Float16* hs = m->hs + (size_t)a0 * HIDDEN;
+  float* ps = m->ps + (size_t)a0 * ATT_K;
+  float* xs = m->xs + (size_t)a0 * HIDDEN;
+  TRY(dh_gather_rows_f16(m->ctx, s, (const uint16_t*)m->h, rowmap, (uint16_t*)hs, n, HIDDEN));
   // rows 0..ATT_K of w_in are q|gate
-  TRY(gemm(m, s, m->hs, HIDDEN, w_in, HIDDEN, m->ps, ATT_K, n, ATT_K, HIDDEN, DH_EPI_STORE_F32));
-  TRY(dh_q_norm_rope(m->ctx, s, m->ps, as<float>(L.q_norm->ptr), m->inv_freq, ans_rows, (uint16_t*)m->qo, n, ATT_K));
+  TRY(gemm(m, s, hs, HIDDEN, w_in, HIDDEN, ps, ATT_K, n, ATT_K, HIDDEN, DH_EPI_STORE_F32));
+  TRY(dh_q_norm_rope(m->ctx, s, ps, as<float>(L.q_norm->ptr), m->inv_freq, qpos, (uint16_t*)m->qo, n, ATT_K));
   TRY(dh_attention(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
-                   (const uint16_t*)m->vc[L.att_index], m->ps, ans_rows, (uint16_t*)m->g, n, ATT_K));
-  TRY(dh_gather_rows_f32(m->ctx, s, m->x, ans_rows, m->xs, n, HIDDEN));
-  TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, m->xs, HIDDEN, n, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
-  return mlp(m, s, L, m->xs, m->hs, n);
+                   (const uint16_t*)m->vc[L.att_index], ps, qpos, (uint16_t*)m->g, n, ATT_K));
+  TRY(dh_gather_rows_f32(m->ctx, s, m->x, rowmap, xs, n, HIDDEN));
+  TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, xs, HIDDEN, n, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
+  TRY(mlp(m, s, L, xs, hs, n));
+  return final_head(m, s, r, ch);
 }
 
 }  // namespace
+
+int dh_model_impl::encode_chunk(dh_model* m, void* s, const RunArgs& r, const Chunk& ch, Source src,
+                                const StateEntry* capture, bool prune) {
+  TRY(dh_embed_bf16(m->ctx, s, r.ids + ch.stage_row, (const uint16_t*)m->embed->ptr, m->x, ch.rows, HIDDEN));
+  const uint32_t last = m->cfg.layers - 1;
+  prune = prune && is_full_attention(last);
+  for (uint32_t l = 0; l < last; ++l) TRY(layer_full(m, s, m->layers[l], ch, src, capture));
+  if (prune) return layer_pruned(m, s, m->layers[last], r, ch);
+  TRY(layer_full(m, s, m->layers[last], ch, src, capture));
+  if (ch.n == 0) return ok();
+  TRY(dh_gather_rows_f32(m->ctx, s, m->x, r.ans_rows + ch.a0, m->xs + (size_t)ch.a0 * HIDDEN, ch.n, HIDDEN));
+  return final_head(m, s, r, ch);
+}
 
 extern "C" {
 
@@ -237,7 +247,7 @@ int dh_model_create(dh_ctx* ctx, const dh_model_config* cfg, dh_model** out) {
   // A_log N(0.5, 0.5) and dt_bias N(0, 0.5), all fp32 (decide keeps them fp32).
   m->embed = add("embed", (uint64_t)cfg->vocab * HIDDEN, BF16, 0.f, 0.02f);
   m->final_norm = add("final_norm", HIDDEN, F32, 0.f, 0.02f);
-  uint32_t n_att = 0;
+  uint32_t n_att = 0, n_lin = 0;
   for (uint32_t l = 0; l < cfg->layers && okay; ++l) {
     Layer L;
     const std::string pre = "L" + std::to_string(l) + ".";
@@ -250,6 +260,7 @@ int dh_model_create(dh_ctx* ctx, const dh_model_config* cfg, dh_model** out) {
       L.k_norm = add(pre + "k_norm", HEAD_DIM, F32, 0.f, 0.02f);
       L.w_out = add(pre + "w_out", (uint64_t)HIDDEN * Q_DIM, F16, 0.f, 0.02f);
     } else {
+      L.lin_index = n_lin++;
       L.w_in = add(pre + "w_in", (uint64_t)LIN_IN_N * HIDDEN, F16, 0.f, 0.02f);
       L.conv_w = add(pre + "conv_w", (uint64_t)CONV_DIM * CONV_K, F32, 0.f, 0.3f);
       L.a_log = add(pre + "a_log", NV, F32, 0.5f, 0.5f);
@@ -282,14 +293,28 @@ int dh_model_create(dh_ctx* ctx, const dh_model_config* cfg, dh_model** out) {
       m->kc.push_back((_Float16*)buf((uint64_t)T * KV_DIM * 2));
       m->vc.push_back((_Float16*)buf((uint64_t)T * KV_DIM * 2));
     }
-    m->zero_state = (float*)buf((uint64_t)NV * DV * DK * 4);
-    m->zero_conv = (float*)buf((uint64_t)3 * CONV_DIM * 4);
+    for (uint32_t i = 0; i < n_lin; ++i) {
+      m->state.push_back((float*)buf(kStateBytes));
+      m->conv.push_back((float*)buf(kConvBytes));
+    }
+    m->zero_state = (float*)buf(kStateBytes);
+    m->zero_conv = (float*)buf(kConvBytes);
     m->iota = (uint32_t*)buf((uint64_t)T * 4);
     m->inv_freq = (float*)buf(ROT_HALF * 4);
     m->xs = (float*)buf((uint64_t)A * HIDDEN * 4);
     m->hs = (_Float16*)buf((uint64_t)A * HIDDEN * 2);
     m->ps = (float*)buf((uint64_t)A * ATT_K * 4);
+    m->req_ids = (uint32_t*)buf((uint64_t)T * 4);
+    m->req_rows = (uint32_t*)buf((uint64_t)A * 4);
+    m->req_pos = (uint32_t*)buf((uint64_t)A * 4);
+    m->req_cand = (uint32_t*)buf((uint64_t)A * cfg->max_cand * 4);
+    m->req_ncand = (uint32_t*)buf((uint64_t)A * 4);
+    m->req_logits = (float*)buf((uint64_t)A * cfg->max_cand * 4);
   }
+  m->n_att = n_att;
+  m->n_lin = n_lin;
+  m->chunk = T;
+  m->state_marker.assign(kStateMarker, kStateMarker + 4);
   if (!okay) {
     delete m;
     return fail(DH_ENOMEM, "model: device allocation failed");
@@ -300,8 +325,7 @@ int dh_model_create(dh_ctx* ctx, const dh_model_config* cfg, dh_model** out) {
   for (uint32_t i = 0; i < ROT_HALF; ++i) inv_freq[i] = 1.0f / powf(1e7f, (float)(2 * i) / 64.0f);  // config.rs:43-46
   if (hipMemcpy(m->iota, iota.data(), (size_t)T * 4, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(m->inv_freq, inv_freq, sizeof inv_freq, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(m->zero_state, 0, (size_t)NV * DV * DK * 4) != hipSuccess ||
-      hipMemset(m->zero_conv, 0, (size_t)3 * CONV_DIM * 4) != hipSuccess) {
+      hipMemset(m->zero_state, 0, kStateBytes) != hipSuccess || hipMemset(m->zero_conv, 0, kConvBytes) != hipSuccess) {
     delete m;
     return fail(DH_EDEVICE, "model: initialising constant buffers failed");
   }
@@ -346,20 +370,18 @@ int dh_model_forward(dh_model* m, void* stream, const uint32_t* ids, uint32_t t,
   if (n_ans > m->cfg.max_answers)
     return fail(DH_EINVAL, "forward: %u answers exceed the model's %u", n_ans, m->cfg.max_answers);
   if (!ids || (n_ans && (!ans_rows || !cand || !ncand || !logits))) return fail(DH_EINVAL, "forward: null pointer");
-  const bool prune = (flags & DH_FORWARD_NO_PRUNE) == 0 && is_full_attention(m->cfg.layers - 1);
-  void* s = stream;
-  TRY(dh_embed_bf16(m->ctx, s, ids, (const uint16_t*)m->embed->ptr, m->x, t, HIDDEN));
-  const uint32_t last = m->cfg.layers - 1;
-  for (uint32_t l = 0; l < m->cfg.layers; ++l) {
-    if (l == last && prune)
-      TRY(layer_pruned(m, s, m->layers[l], t, ans_rows, n_ans));
-    else
-      TRY(layer_full(m, s, m->layers[l], t));
-  }
-  if (n_ans == 0) return ok();
-  if (!prune) TRY(dh_gather_rows_f32(m->ctx, s, m->x, ans_rows, m->xs, n_ans, HIDDEN));
-  return dh_final_head(m->ctx, s, m->xs, as<float>(m->final_norm->ptr), (const uint16_t*)m->embed->ptr, cand, ncand,
-                       logits, n_ans, HIDDEN, m->cfg.max_cand, EPS);
+  // the full route as one chunk of all t rows from zero state; answer rows are their positions
+  RunArgs r;
+  r.ids = ids;
+  r.ans_rows = ans_rows;
+  r.ans_pos = ans_rows;
+  r.cand = cand;
+  r.ncand = ncand;
+  r.logits = logits;
+  Chunk ch;
+  ch.rows = t;
+  ch.n = n_ans;
+  return encode_chunk(m, stream, r, ch, Source{}, nullptr, (flags & DH_FORWARD_NO_PRUNE) == 0);
 }
 
 int dh_model_capture(dh_model* m, void* stream, const uint32_t* ids, uint32_t t, const uint32_t* ans_rows,

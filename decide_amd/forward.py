@@ -2,8 +2,10 @@
 
 The model owns its weights and activation buffers in device memory (``dh_model_create``), named as in
 decide's ``decide-weights-v1`` index (convert.rs:158-245). ``forward`` enqueues one full-route forward
-(embedding, every layer, the pruned last layer, the candidate head) on a stream; nothing here computes
-anything itself.
+(embedding, every layer, the pruned last layer, the candidate head) on a stream. The request methods
+(``logits``, ``build_snapshot``, the state cache; forward.rs:641-1116) take host ids and answers, run in
+chunks from the prefix snapshot or a cached state, and wait for their result, as decide's do. Nothing
+here computes anything itself.
 """
 
 from __future__ import annotations
@@ -17,6 +19,29 @@ from . import _lib
 from .kernels import Arg, Context, _call, addr
 
 DTYPES = {0: np.float16, 1: np.uint16, 2: np.float32}  # bf16 weights are returned as raw bits
+
+# decide's Route (forward.rs:196-207)
+ROUTES = {_lib.DH_ROUTE_SNAPSHOT: "snapshot", _lib.DH_ROUTE_FULL: "full", _lib.DH_ROUTE_STATE_CACHE: "state_cache"}
+MAX_STATE_ENTRIES = 4  # forward.rs:70
+STATE_MARKER = (550, 39087, 10485, 198)  # forward.rs:68
+
+
+def _u32(values) -> ctypes.Array:
+    a = np.ascontiguousarray(np.asarray(values, dtype=np.int64))
+    if a.size and (a.min() < 0 or a.max() > 0xFFFFFFFF):
+        raise ValueError("ids must be unsigned 32-bit")
+    return (ctypes.c_uint32 * max(a.size, 1))(*a.tolist())
+
+
+def state_boundary(ids, prefix: int, marker, limit: int):
+    """Where a prompt's state ends: one past the first ``marker`` in ``ids[prefix:limit]``, or None
+    (decide: state_boundary, forward.rs:1503-1515). Host code of the library, no GPU involved."""
+    lib = _lib.load()
+    ids, marker = list(ids), list(marker)
+    b, found = ctypes.c_uint32(), ctypes.c_int()
+    _call(lib.dh_state_boundary(_u32(ids), len(ids), prefix, _u32(marker), len(marker), limit, ctypes.byref(b),
+                                ctypes.byref(found)))
+    return int(b.value) if found.value else None
 
 
 @dataclass
@@ -105,6 +130,83 @@ class Model:
                                         addr(cand), addr(ncand), addr(logits), flags))
 
 
+    # ---- requests (decide: Forward, forward.rs:641-1116); host ids, synchronous
+    def logits(self, stream: int, ids, answers, full: bool = False) -> list[list[float]]:
+        """Logits of each answer's candidates: ``answers`` is a list of (absolute logit row, candidate ids);
+        one row of logits per answer, in the given order (decide: logits / logits_full, forward.rs:696-815)."""
+        ids = list(ids)
+        arr = (_lib.DhAnswer * max(len(answers), 1))()
+        keep = []
+        for i, (row, cand) in enumerate(answers):
+            c = _u32(list(cand))
+            keep.append(c)
+            arr[i].row = int(row)
+            arr[i].ncand = len(cand)
+            arr[i].cand = ctypes.cast(c, ctypes.POINTER(ctypes.c_uint32))
+        mc = self.cfg.max_cand
+        out = np.full(max(len(answers), 1) * mc, np.nan, dtype=np.float32)
+        flags = _lib.DH_LOGITS_FULL if full else 0
+        _call(self.lib.dh_model_logits(self.handle, ctypes.c_void_p(stream), _u32(ids), len(ids), arr, len(answers),
+                                       out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), flags))
+        return [out[i * mc:i * mc + len(c)].tolist() for i, (_, c) in enumerate(answers)]
+
+    def logits_full(self, stream: int, ids, answers) -> list[list[float]]:
+        """``logits`` by the full path whatever the ids (decide: logits_full, forward.rs:809-815)."""
+        return self.logits(stream, ids, answers, full=True)
+
+    def build_snapshot(self, stream: int, prefix_ids) -> None:
+        """Run the constant prompt prefix from zero state and keep the state after it (forward.rs:641-675)."""
+        ids = list(prefix_ids)
+        _call(self.lib.dh_model_build_snapshot(self.handle, ctypes.c_void_p(stream), _u32(ids), len(ids)))
+
+    def prefix_len(self):
+        n, has = ctypes.c_uint32(), ctypes.c_int()
+        _call(self.lib.dh_model_prefix_len(self.handle, ctypes.byref(n), ctypes.byref(has)))
+        return int(n.value) if has.value else None
+
+    def last_route(self):
+        """"snapshot", "full" or "state_cache" for the last ``logits`` call (None before the first)."""
+        r, s = ctypes.c_int32(), ctypes.c_int64()
+        _call(self.lib.dh_model_last_route(self.handle, ctypes.byref(r), ctypes.byref(s)))
+        return ROUTES.get(r.value)
+
+    def last_start(self):
+        """The first position the last ``logits`` call computed (forward.rs:688-694)."""
+        r, s = ctypes.c_int32(), ctypes.c_int64()
+        _call(self.lib.dh_model_last_route(self.handle, ctypes.byref(r), ctypes.byref(s)))
+        return None if s.value < 0 else int(s.value)
+
+    def chunk(self) -> int:
+        return int(self.lib.dh_model_chunk(self.handle))
+
+    def set_chunk(self, rows: int) -> None:
+        _call(self.lib.dh_model_set_chunk(self.handle, rows))
+
+    def pruning(self) -> bool:
+        return bool(self.lib.dh_model_pruning(self.handle))
+
+    def set_pruning(self, on: bool) -> None:
+        self.lib.dh_model_set_pruning(self.handle, 1 if on else 0)
+
+    def set_state_cache(self, entries: int) -> None:
+        _call(self.lib.dh_model_set_state_cache(self.handle, entries))
+
+    def state_cache_capacity(self) -> int:
+        return int(self.lib.dh_model_state_cache_capacity(self.handle))
+
+    def forget_states(self) -> None:
+        self.lib.dh_model_forget_states(self.handle)
+
+    def cached_states(self) -> list[int]:
+        buf = (ctypes.c_uint32 * MAX_STATE_ENTRIES)()
+        n = self.lib.dh_model_cached_states(self.handle, buf, MAX_STATE_ENTRIES)
+        return [int(buf[i]) for i in range(min(n, MAX_STATE_ENTRIES))]
+
+    def set_state_marker(self, marker) -> None:
+        m = list(marker)
+        _call(self.lib.dh_model_set_state_marker(self.handle, _u32(m), len(m)))
+
+
 class Graph:
     """A captured whole forward (dh_model_capture): one launch replays every kernel of the forward."""
 
@@ -142,10 +244,11 @@ def main():
     ap.add_argument("--tokens", type=int, default=2307)
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--no-prune", action="store_true")
+    ap.add_argument("--delta-chunked", action="store_true", help="chunked gated delta recurrence (DH_DELTA_CHUNKED)")
     args = ap.parse_args()
     if not hip.available():
         raise SystemExit("no GPU")
-    k = Kernels()
+    k = Kernels(delta_chunked=args.delta_chunked)
     st = Stream()
     s = st.handle
     t = args.tokens
@@ -166,7 +269,8 @@ def main():
         e1.synchronize()
         if i:
             times.append(e0.elapsed_ms(e1))
-    print(json.dumps({"layers": args.layers, "tokens": t, "runs": args.runs, "p50_ms": float(np.median(times)),
+    print(json.dumps({"layers": args.layers, "tokens": t, "runs": args.runs, "delta_chunked": args.delta_chunked,
+                      "p50_ms": float(np.median(times)),
                       "logits": logits.numpy().round(4).tolist()}), flush=True)
     model.close()
 

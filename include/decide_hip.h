@@ -250,10 +250,11 @@ int dh_fill_normal(dh_ctx* ctx, void* stream, void* out, uint64_t n, uint64_t se
 /* ======================================================================
  * The hybrid decoder forward (decide: Forward, crates/decide-engine/src/
  * forward.rs): the host that strings the kernels above into decide's layer
- * order with its buffers and fp16 rounding points, over one stream. It runs
- * the full route from position 0 as one chunk of all T rows, and prunes the
- * last layer (full attention) to the answer rows as decide does
- * (forward.rs:1144-1187). Weights live in device memory the model owns, named
+ * order with its buffers and fp16 rounding points, over one stream.
+ * dh_model_forward runs the full route from position 0 as one chunk of all
+ * T rows, and prunes the last layer (full attention) to the answer rows as
+ * decide does (forward.rs:1133-1187); the request calls further down add
+ * chunking, the prefix snapshot and the state cache. Weights live in device memory the model owns, named
  * as in decide's decide-weights-v1 index (convert.rs:158-245): "embed" (bf16
  * [vocab, 2560]), "final_norm", "L{l}.in_norm", "L{l}.w_in", "L{l}.w_out",
  * "L{l}.post_norm", "L{l}.w_gu", "L{l}.w_down", and per layer kind
@@ -313,6 +314,81 @@ int dh_model_capture(dh_model* model, void* stream, const uint32_t* ids, uint32_
                      dh_graph** out);
 int dh_graph_launch(dh_graph* graph, void* stream);
 void dh_graph_destroy(dh_graph* graph);
+
+/* ======================================================================
+ * Requests (decide: Forward::logits, build_snapshot and the state cache,
+ * crates/decide-engine/src/forward.rs:641-1116). Host ids and answers; each
+ * call enqueues its work on `stream` and waits for it, as decide's do.
+ *   - Chunks: a span runs in chunks of at most dh_model_chunk() rows, every
+ *     layer of one chunk and then the next, state carried between chunks
+ *     (forward.rs:887-915). Default: max_tokens (the whole span in one
+ *     chunk); decide's default is CHUNK = 512 (config.rs:36).
+ *   - Prefix snapshot: dh_model_build_snapshot runs the constant prompt
+ *     prefix from zero state and keeps the state after it.
+ *   - Tail truncation: rows after the last answer row never run.
+ *   - State cache: an LRU of up to 4 states (default 2) at the end of
+ *     prompts' state sections, which end with the state marker (default
+ *     decide's STATE_MARKER, forward.rs:68). A request about a new state
+ *     captures it on the way; one whose ids start with a cached state's ids
+ *     runs from the end of that state.
+ * ====================================================================== */
+typedef struct dh_answer {
+  uint32_t row;          /* absolute logit row (< the request's token count) */
+  uint32_t ncand;        /* 1 .. max_cand */
+  const uint32_t* cand;  /* host candidate token ids [ncand], each < vocab */
+} dh_answer;
+
+/* dh_model_logits flags */
+#define DH_LOGITS_FULL 1u /* the full route whatever the ids (decide: logits_full, forward.rs:809-815) */
+
+/* dh_model_last_route routes (decide: Route, forward.rs:196-207) */
+#define DH_ROUTE_SNAPSHOT 0
+#define DH_ROUTE_FULL 1
+#define DH_ROUTE_STATE_CACHE 2
+
+/* Logits of each answer's candidates into logits[i * max_cand + c] for the
+ * caller's answer i and c < answers[i].ncand (other entries untouched).
+ * Checks decide's contract with its messages (check_ids, sorted_answers,
+ * forward.rs:1494-1541) and refuses non-finite logits (forward.rs:876-882).
+ * Route: from the snapshot when the ids start with the prefix and every
+ * answer row lies after it, from a cached state when the ids also start
+ * with that state's ids (the longest such), else the full route
+ * (decide: logits, forward.rs:696-735; run_answers, 817-885). */
+int dh_model_logits(dh_model* model, void* stream, const uint32_t* ids, uint32_t len, const dh_answer* answers,
+                    uint32_t n_answers, float* logits, uint32_t flags);
+/* Runs `prefix_ids` (len < max_tokens) from position 0 with zero state and
+ * keeps the state after it; replaces any earlier snapshot and empties the
+ * state cache (decide: build_snapshot, forward.rs:641-675). */
+int dh_model_build_snapshot(dh_model* model, void* stream, const uint32_t* prefix_ids, uint32_t len);
+/* The snapshot's prefix length (*has_snapshot 0 before the first build;
+ * decide: prefix_len, forward.rs:677-680). */
+int dh_model_prefix_len(const dh_model* model, uint32_t* len, int* has_snapshot);
+/* How the last dh_model_logits computed its request (DH_ROUTE_*, or -1
+ * before the first) and the first position it computed (decide: last_route,
+ * last_start, forward.rs:682-694). */
+int dh_model_last_route(const dh_model* model, int32_t* route, int64_t* start);
+/* Rows per chunk, 1 .. max_tokens (decide: set_chunk, forward.rs:560-566). */
+int dh_model_set_chunk(dh_model* model, uint32_t rows);
+uint32_t dh_model_chunk(const dh_model* model);
+/* Prune the last layer to the answer rows (default on; decide: set_pruning, forward.rs:573-578). */
+void dh_model_set_pruning(dh_model* model, int on);
+int dh_model_pruning(const dh_model* model);
+/* State cache capacity, 0 .. 4 (0 turns it off); shrinking evicts the least
+ * recently used entries (decide: set_state_cache, forward.rs:732-743). */
+int dh_model_set_state_cache(dh_model* model, uint32_t entries);
+uint32_t dh_model_state_cache_capacity(const dh_model* model);
+/* Forget every cached state, keeping the buffers for the next captures (forward.rs:745-750). */
+void dh_model_forget_states(dh_model* model);
+/* The token length of each cached state, most recently used first, into
+ * lens[0 .. max); returns the number of entries (decide: cached_states, forward.rs:757-762). */
+uint32_t dh_model_cached_states(const dh_model* model, uint32_t* lens, uint32_t max);
+/* The ids that end a prompt's state; empties the cache (decide: set_state_marker, forward.rs:764-771). */
+int dh_model_set_state_marker(dh_model* model, const uint32_t* marker, uint32_t len);
+/* Where a prompt's state ends: one past the first `marker` in
+ * ids[prefix .. min(limit, len)]; *found 0 if there is none (decide:
+ * state_boundary, forward.rs:1503-1515). Host-only. */
+int dh_state_boundary(const uint32_t* ids, uint32_t len, uint32_t prefix, const uint32_t* marker, uint32_t marker_len,
+                      uint32_t limit, uint32_t* boundary, int* found);
 
 #ifdef __cplusplus
 }
