@@ -21,6 +21,8 @@ DH_EDEVICE = 4
 
 DH_GEMM_REFERENCE = 1
 DH_DELTA_CHUNKED = 2
+DH_DELTA_SEQUENTIAL = 4
+DH_DELTA_CHUNK_MIN_T = 320
 
 
 class DhGemmMember(ctypes.Structure):

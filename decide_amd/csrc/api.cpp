@@ -169,7 +169,9 @@ const char* dh_version(void) { return "decide-hip 0.1.0 (gfx950, fp16 MFMA 16x16
 int dh_ctx_create(uint32_t flags, dh_ctx** out) {
   if (!out) return fail(DH_EINVAL, "dh_ctx_create: out is NULL");
   *out = nullptr;
-  if (flags & ~(DH_GEMM_REFERENCE | DH_DELTA_CHUNKED))
+  if ((flags & DH_DELTA_CHUNKED) && (flags & DH_DELTA_SEQUENTIAL))
+    return fail(DH_EINVAL, "ctx_create: DH_DELTA_CHUNKED and DH_DELTA_SEQUENTIAL exclude each other");
+  if (flags & ~(DH_GEMM_REFERENCE | DH_DELTA_CHUNKED | DH_DELTA_SEQUENTIAL))
     return fail(DH_EINVAL, "dh_ctx_create: unknown flags 0x%x", flags);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -312,7 +314,9 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
     int rc = ensure_ws(ctx, need);
     if (rc != DH_OK) return rc;
   }
-  if (ctx->flags & DH_DELTA_CHUNKED) {  // the chunked recurrence's workspace for max_m tokens
+  const bool chunked = (ctx->flags & DH_DELTA_CHUNKED) ||
+                       (!(ctx->flags & DH_DELTA_SEQUENTIAL) && max_m >= DH_DELTA_CHUNK_MIN_T);
+  if (chunked) {  // the chunked recurrence's workspace for max_m tokens
     int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(std::max(1u, max_m)) * sizeof(float));
     if (rc != DH_OK) return rc;
   }

@@ -65,7 +65,9 @@ int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, co
   if (misaligned(q, 16) || misaligned(k, 16) || misaligned(state_in, 16) || misaligned(state_out, 16))
     return fail(DH_EINVAL, "delta: q, k and the states must be 16-byte aligned");
   if (!ctx) return fail(DH_EINVAL, "delta: null context");
-  if (!(ctx->flags & DH_DELTA_CHUNKED)) {
+  const bool chunked = (ctx->flags & DH_DELTA_CHUNKED) ||
+                       (!(ctx->flags & DH_DELTA_SEQUENTIAL) && t >= DH_DELTA_CHUNK_MIN_T);
+  if (!chunked) {
     mark(ctx, kKidDelta);
     return hip_status(dh::launch_gated_delta(q, k, v, a, b, a_log, dt_bias, state_in, state_out, o, t, ldab,
                                              write_state != 0, (hipStream_t)stream),

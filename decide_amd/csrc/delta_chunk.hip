@@ -8,33 +8,43 @@
 // no γ under/overflows):
 //   A_ij = β_i (γ_i/γ_j) k_i·k_j (i > j),   T = (I + A)⁻¹,
 //   W = T diag(βγ) K,   U = T diag(β) V,   M_ij = (γ_i/γ_j) q_i·k_j (i ≥ j),
-// then, sequentially over chunks with the state S (DV × DK) of the chunk start,
-//   V' = U − W Sᵀ,   O = diag(γ) Q Sᵀ + M V',   S ← γ_C S + V'ᵀ diag(γ_C/γ) K.
-// Kernel 1 (prep) computes A, T, W, U, M for every (chunk, value head) in
-// parallel; kernel 2 (scan) runs the chunks in order for each (head, 32 value
-// rows). Tokens past T in the last chunk enter with k = q = v = 0, β = 0 and
+// then, in chunk order, with the state S (DV × DK) at the chunk start,
+//   V' = U − W Sᵀ,   S ← γ_C S + V'ᵀ diag(γ_C/γ) K,
+// and, for every chunk independently once its S and V' are known,
+//   O = diag(γ) Q Sᵀ + M V'.
+// Three kernels:
+//   prep: W, U, M and K̃ᵀ = (diag(γ_C/γ) K)ᵀ for every (chunk, value head);
+//   scan: the chunks in order for each (head, 16 value rows), keeping the
+//         state slice in LDS; it stores each chunk's starting S and V';
+//   out:  O for every (chunk, head, 32 value columns).
+// Tokens past T in the last chunk enter with k = q = v = 0, β = 0 and
 // log g = 0, so they change nothing.
-#include <type_traits>
-
+//
+// MFMA operand feed: every product is written as D = Σ_k A[i][k] B[j][k] over
+// LDS tiles whose rows are k-contiguous. Because the sum is over k, lane
+// (r = l % 16, g = l / 16) may hold any k as long as A and B agree: here lane
+// group g holds the contiguous k range [g·K/4, (g + 1)·K/4), so each lane
+// reads its operands with ds_read_b128, all before the MFMAs. Row strides of
+// 4 (mod 64) floats make those reads conflict-free.
 #include "dh_kernels.h"
 
 namespace dh {
 
 namespace {
 
-constexpr int C = 64;            // tokens per chunk
+constexpr int C = 64;  // tokens per chunk
 constexpr int NK = 16, DK = 128, NV = 32, DV = 128;
-// LDS row strides, in floats, for 64 banks of 4 bytes. A tile read as an
-// MFMA operand with lane (r, g) at [16 m + r][4 n + g] needs a stride of 4
-// (mod 64) to be conflict-free; one read at [4 n + g][16 m + r] (the B
-// operand of a product over the tile's rows) needs 16 (mod 64).
-constexpr int LDF = DK + 4;      // 64 × 128 tiles read along rows
-constexpr int LDK = DK + 16;     // 64 × 128 tiles read down columns
-constexpr int LDT = C + 4;       // 64 × 64 triangular tiles
-constexpr int LDM = C + 4;
-// workspace layout per (chunk, value head), in floats
-constexpr int kOffW = 0, kOffU = C * DK, kOffM = 2 * C * DK, kOffGam = 2 * C * DK + C * C, kOffRho = kOffGam + C;
-constexpr int kWsStride = kOffRho + C;
+constexpr int LDF = DK + 4;  // row stride of [.][128] LDS tiles
+constexpr int LDT = C + 4;   // row stride of [.][64] LDS tiles
+// workspace per (chunk, value head), in floats
+constexpr int kOffW = 0;                  // W [64][128]
+constexpr int kOffU = kOffW + C * DK;     // U [64][128]
+constexpr int kOffM = kOffU + C * DK;     // M [64][64]
+constexpr int kOffKt = kOffM + C * C;     // K̃ᵀ [128][64]
+constexpr int kOffGam = kOffKt + DK * C;  // γ [64]
+constexpr int kOffVt = kOffGam + C;       // V'ᵀ [128][64] (scan → out)
+constexpr int kOffS = kOffVt + DV * C;    // S at the chunk start [128][128] (scan → out)
+constexpr int kWsStride = kOffS + DV * DK;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -50,6 +60,31 @@ __device__ __forceinline__ void sfor(Fn&& fn) {
   }
 }
 
+// acc += Σ_k A[r][k] B[r][k] over KLEN, A and B pointing at the tiles' first
+// rows (16 rows each); lane (r, g) covers k in [g·KLEN/4, (g + 1)·KLEN/4).
+template <int KLEN>
+__device__ __forceinline__ f4 nt_tile(const float* A, int lda, const float* B, int ldb, int r, int g, f4 acc) {
+  constexpr int P = KLEN / 4;
+  f4 a[P / 4], b[P / 4];
+  const float* pa = A + r * lda + g * P;
+  const float* pb = B + r * ldb + g * P;
+#pragma unroll
+  for (int q = 0; q < P / 4; ++q) {
+    a[q] = *(const f4*)(pa + 4 * q);
+    b[q] = *(const f4*)(pb + 4 * q);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep every read ahead of the MFMAs (the scheduler would interleave them)
+  f4 acc2 = f4{0.f, 0.f, 0.f, 0.f};  // two independent chains, summed at the end
+#pragma unroll
+  for (int q = 0; q < P / 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      acc = mfma4(a[q][e], b[q][e], acc);
+      acc2 = mfma4(a[q][e + 1], b[q][e + 1], acc2);
+    }
+  return acc + acc2;
+}
+
 // Rows t0 .. t0 + 63 of a [T][heads][128] fp32 tensor (head `hd`), zero past
 // T: thread tid holds float4 number tid + 256 n, row (tid + 256 n) / 32.
 __device__ __forceinline__ void fetch_rows(f4 (&x)[8], const float* __restrict__ src, uint32_t t0, uint32_t T,
@@ -61,12 +96,11 @@ __device__ __forceinline__ void fetch_rows(f4 (&x)[8], const float* __restrict__
   }
 }
 
-template <int LD>
 __device__ __forceinline__ void stage_rows(float* dst, const f4 (&x)[8], int tid) {
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     const int e = tid + 256 * n, i = e >> 5, d4 = (e & 31) * 4;
-    *(f4*)(dst + i * LD + d4) = x[n];
+    *(f4*)(dst + i * LDF + d4) = x[n];
   }
 }
 
@@ -78,6 +112,8 @@ __device__ __forceinline__ void lower_block(int p, int& i, int& j) {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// prep: one workgroup per (chunk, value head).
 __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                                const float* __restrict__ v, const float* __restrict__ a,
                                                                const float* __restrict__ b, uint32_t ldab,
@@ -85,25 +121,24 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
                                                                const float* __restrict__ dt_bias, float* __restrict__ ws,
                                                                uint32_t T) {
   __shared__ __attribute__((aligned(16))) float Ks[C * LDF];
-  __shared__ __attribute__((aligned(16))) float Qs[C * LDF];
-  __shared__ __attribute__((aligned(16))) float Vs[C * LDK];
-  __shared__ float As[C * LDT];
-  __shared__ float Ts[C * LDT];
-  __shared__ float Lg[C], Bt[C], Gm[C];
+  __shared__ __attribute__((aligned(16))) float QVs[C * LDF];  // Q, then V
+  __shared__ __attribute__((aligned(16))) float As[C * LDT];
+  __shared__ __attribute__((aligned(16))) float Ts[C * LDT];
+  __shared__ __attribute__((aligned(16))) float Lg[C], Bt[C], Gm[C], SCw[C], Rh[C];
   __shared__ float Ysc[4 * 16 * 17];  // per-wave 16 × 16 scratch of the blocked inversion
   const uint32_t c = blockIdx.x, h = blockIdx.y, hk = h >> 1, t0 = c * C;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, g4 = lane >> 4;
+  const int r = lane & 15, g = lane >> 4;
   float* out = ws + ((size_t)c * NV + h) * kWsStride;
 
-  {  // all 24 loads in flight before the first LDS store
-    f4 xk[8], xq[8], xv[8];
+  f4 xv[8];
+  {  // all loads in flight before the first LDS store; V waits in registers until Q is done
+    f4 xk[8], xq[8];
     fetch_rows(xk, k, t0, T, NK, hk, tid);
     fetch_rows(xq, q, t0, T, NK, hk, tid);
     fetch_rows(xv, v, t0, T, NV, h, tid);
-    stage_rows<LDF>(Ks, xk, tid);
-    stage_rows<LDF>(Qs, xq, tid);
-    stage_rows<LDK>(Vs, xv, tid);
+    stage_rows(Ks, xk, tid);
+    stage_rows(QVs, xq, tid);
   }
   if (wave == 0) {
     const uint32_t t = t0 + lane;
@@ -117,37 +152,49 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
       const float y = __shfl_up(lam, o, 64);
       if (lane >= o) lam += y;
     }
+    const float last = __shfl(lam, 63, 64);
+    const float gm = expf(lam);
     Lg[lane] = lam;
     Bt[lane] = bt;
-    Gm[lane] = expf(lam);
+    Gm[lane] = gm;
+    SCw[lane] = bt * gm;
+    Rh[lane] = expf(last - lam);
   }
   __syncthreads();
 
   // K Kᵀ → A (strictly lower, β_i γ_i/γ_j), Q Kᵀ → M (lower incl. diagonal, γ_i/γ_j): the 2 × 10 blocks
-  // of 16 × 16 on or below the diagonal; M's blocks above it are written as zeros, A's are never read
+  // on or below the diagonal; M's blocks above it are written as zeros, A's are never read
   for (int tt = wave; tt < 20; tt += 4) {
     const bool isq = tt >= 10;
     int ti, tj;
     lower_block(isq ? tt - 10 : tt, ti, tj);
-    const float* L = isq ? Qs : Ks;
-    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int kk = 0; kk < DK; kk += 4)
-      acc = mfma4(L[(16 * ti + r16) * LDF + kk + g4], Ks[(16 * tj + r16) * LDF + kk + g4], acc);
-    const int j = 16 * tj + r16;
+    const f4 acc = nt_tile<DK>((isq ? QVs : Ks) + 16 * ti * LDF, LDF, Ks + 16 * tj * LDF, LDF, r, g,
+                               f4{0.f, 0.f, 0.f, 0.f});
+    const int j = 16 * tj + r;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i = 16 * ti + 4 * g4 + e;
-      const float r = i >= j ? expf(Lg[i] - Lg[j]) : 0.f;
+      const int i = 16 * ti + 4 * g + e;
+      const float rr = i >= j ? expf(Lg[i] - Lg[j]) : 0.f;
       if (!isq)
-        As[i * LDT + j] = i > j ? Bt[i] * r * acc[e] : 0.f;
+        As[i * LDT + j] = i > j ? Bt[i] * rr * acc[e] : 0.f;
       else
-        out[kOffM + i * C + j] = r * acc[e];
+        out[kOffM + i * C + j] = rr * acc[e];
     }
   }
   for (int e = tid; e < C * C; e += 256)
     if ((e & 63) >> 4 > e >> 10) out[kOffM + e] = 0.f;
-  __syncthreads();
+  // K̃ᵀ[d][j] = (γ_C/γ_j) K[j][d] for the scan
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int e = tid + 256 * n, d = e >> 4, j4 = (e & 15) * 4;
+    f4 x;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = Rh[j4 + u] * Ks[(j4 + u) * LDF + d];
+    *(f4*)(out + kOffKt + d * C + j4) = x;
+  }
+  if (tid < C) out[kOffGam + tid] = Gm[tid];
+  __syncthreads();  // Q is done: V takes its place
+  stage_rows(QVs, xv, tid);
 
   // T = (I + A)⁻¹, blocked 4 × 4 over 16 × 16 blocks. Diagonal blocks by forward
   // substitution (wave w, lane j < 16 owns column j of block w); then the
@@ -157,7 +204,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
   for (int e = tid; e < C * LDT; e += 256) Ts[e] = 0.f;
   __syncthreads();
   {
-    const int jb = wave;  // diagonal block
+    const int jb = wave;
     if (lane < 16) {
       float x[16];
       sfor<0, 16>([&](auto ic) {
@@ -183,190 +230,294 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
       for (int kb = j; kb < i; ++kb) {  // Y = Σ_k A_ik T_kj
 #pragma unroll
         for (int kk = 0; kk < 16; kk += 4)
-          y = mfma4(As[(16 * i + r16) * LDT + 16 * kb + kk + g4], Ts[(16 * kb + kk + g4) * LDT + 16 * j + r16], y);
+          y = mfma4(As[(16 * i + r) * LDT + 16 * kb + kk + g], Ts[(16 * kb + kk + g) * LDT + 16 * j + r], y);
       }
       float* Yw = Ysc + wave * 16 * 17;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Yw[(4 * g4 + e) * 17 + r16] = y[e];
+      for (int e = 0; e < 4; ++e) Yw[(4 * g + e) * 17 + r] = y[e];
       __builtin_amdgcn_wave_barrier();
       f4 z = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < 16; kk += 4)
-        z = mfma4(Ts[(16 * i + r16) * LDT + 16 * i + kk + g4], Yw[(kk + g4) * 17 + r16], z);
+      for (int kk = 0; kk < 16; kk += 4) z = mfma4(Ts[(16 * i + r) * LDT + 16 * i + kk + g], Yw[(kk + g) * 17 + r], z);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Ts[(16 * i + 4 * g4 + e) * LDT + 16 * j + r16] = -z[e];
+      for (int e = 0; e < 4; ++e) Ts[(16 * i + 4 * g + e) * LDT + 16 * j + r] = -z[e];
     }
     __syncthreads();
   }
 
-  // W = T diag(βγ) K and U = T diag(β) V: 2 × 32 tiles of 16 × 16; T is lower triangular, so row block
-  // ti sums over tokens j < 16 (ti + 1) only
-  for (int tt = wave; tt < 64; tt += 4) {
-    const bool isu = tt >= 32;
-    const int ti = (tt & 31) >> 3, td = tt & 7;
-    const float* R = isu ? Vs : Ks;
-    const int ld = isu ? LDK : LDF;
-    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-    for (int jj = 0; jj < 16 * (ti + 1); jj += 4) {
-      const int j = jj + g4;
-      const float sc = isu ? Bt[j] : Bt[j] * Gm[j];
-      acc = mfma4(Ts[(16 * ti + r16) * LDT + j], R[j * ld + 16 * td + r16] * sc, acc);
-    }
+  // W = T diag(βγ) K and U = T diag(β) V. Wave w: key/value columns 16 td for td = 2w, 2w + 1. T is lower
+  // triangular, so row block ti sums over token blocks jb ≤ ti; within a block lane group g holds tokens
+  // 16 jb + 4 g .. + 4 (one ds_read_b128 of T and of the scale), and the B operand R[j][16 td + r] is
+  // conflict-free with the row stride of 132 floats.
+#pragma unroll
+  for (int isu = 0; isu < 2; ++isu) {
+    const float* R = isu ? QVs : Ks;
+    const float* sc = isu ? Bt : SCw;
     float* dst = out + (isu ? kOffU : kOffW);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dst[(16 * ti + 4 * g4 + e) * DK + 16 * td + r16] = acc[e];
-  }
-  if (tid < C) {
-    out[kOffGam + tid] = Gm[tid];
-    out[kOffRho + tid] = expf(Lg[C - 1] - Lg[tid]);
+    for (int q2 = 0; q2 < 2; ++q2) {
+      const int d0 = 16 * (2 * wave + q2);
+      sfor<0, 4>([&](auto tic) {
+        constexpr int ti = decltype(tic)::value;
+        f4 ta[ti + 1], sv[ti + 1], rb[ti + 1];
+#pragma unroll
+        for (int jb = 0; jb <= ti; ++jb) {
+          ta[jb] = *(const f4*)(Ts + (16 * ti + r) * LDT + 16 * jb + 4 * g);
+          sv[jb] = *(const f4*)(sc + 16 * jb + 4 * g);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) rb[jb][s] = R[(16 * jb + 4 * g + s) * LDF + d0 + r];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jb = 0; jb <= ti; ++jb)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc = mfma4(ta[jb][s] * sv[jb][s], rb[jb][s], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(16 * ti + 4 * g + e) * DK + d0 + r] = acc[e];
+      });
+    }
   }
 }
 
-// One workgroup of 8 waves per (value head, 32 value rows): the 4 workgroups
-// of a head land on one XCD (their ids are 32 apart), so the per-chunk
-// matrices they all read come from HBM once and from that XCD's L2 after.
-// The state slice S [32][128] stays in LDS across all chunks; the next
-// chunk's matrices are loaded into registers while the current chunk
-// computes. Wave w owns value tile u = w % 2 and token tile w / 2 of V' and
-// O, and key-dim tiles 2 (w / 2), 2 (w / 2) + 1 of the state update.
-constexpr int kScanRows = 32, kScanThreads = 512;
-constexpr int LDV2 = 48;  // V'ᵀ/U tiles [64][32], read down columns
+// ---------------------------------------------------------------------------
+// scan: one workgroup per (value head, 16 value rows); the 8 workgroups of a
+// head have ids 32 apart, so they run on one XCD and share its L2 for the
+// per-chunk matrices. Waves 0-3 compute and touch LDS only; wave 4 does all
+// the global memory work, so that its issue stalls never hold up an MFMA:
+//   chunk c, waves 0-3:  V'ᵀ = Uᵀ − S Wᵀ (wave w: tokens 16 w .. + 16)
+//                        | barrier |
+//                        S = γ_C S + V'ᵀ K̃ (wave w: key columns 32 w .. + 32)
+//   chunk c, wave 4:     DMA chunk c + 1's W, K̃ᵀ and U slice into the other
+//                        LDS buffer; store S (the chunk's starting state)
+//                        | barrier |
+//                        store V'ᵀ; wait for the DMA
+//   | barrier |
+// W and K̃ᵀ land by global→LDS DMA (16 bytes per lane, 1 KB per instruction)
+// in an unpadded layout whose 16-byte chunks are XOR-swizzled by row
+// (chunk c of row r at c ^ (r % 16)), so the MFMA operand reads stay
+// conflict-free.
+constexpr int kScanRows = 16;
 
-namespace {
-struct ScanPrefetch {
-  f4 w[4], q[4], k[4], m[2], u;
-  float gam, rho;
-};
-}  // namespace
+// 16 bytes per lane global → LDS: lane l's 16 bytes at sbase + voff land at
+// LDS byte address lds_byte + 16·l. M0 is written in the same statement (one
+// wait state before its use); nothing else in this file reads M0. Both the
+// LDS address and the base must be wave-uniform: they go through
+// readfirstlane into SGPRs.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_lds(uint32_t lds_byte, uint32_t voff, const void* sbase) {
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint64_t ub = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t ul = __builtin_amdgcn_readfirstlane(lds_byte);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(ul), "v"(voff),
+               "s"((const void*)(uintptr_t)ub)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
-__global__ __launch_bounds__(kScanThreads) void delta_chunk_scan_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ ws, const float* state_in,
-    float* state_out, float* __restrict__ o, uint32_t T, uint32_t write_state) {
-  __shared__ __attribute__((aligned(16))) float Ss[kScanRows * LDF];
-  __shared__ __attribute__((aligned(16))) float Ws[C * LDF];
-  __shared__ __attribute__((aligned(16))) float Qs[C * LDF];
-  __shared__ __attribute__((aligned(16))) float Ks[C * LDK];
-  __shared__ float Ms[C * LDM];
-  __shared__ float Us[C * LDV2];
-  __shared__ float Vp[C * LDV2];
-  __shared__ float Gm[C], Rh[C];
-  const uint32_t h = blockIdx.x, hk = h >> 1, dv0 = blockIdx.y * kScanRows;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, g4 = lane >> 4;
-  const int u = wave & 1, i0 = 16 * (wave >> 1);
-
-  for (int e = tid; e < kScanRows * DK / 4; e += kScanThreads) {
-    const int r = e >> 5, d4 = (e & 31) * 4;
-    *(f4*)(Ss + r * LDF + d4) = *(const f4*)(state_in + ((size_t)h * DV + dv0 + r) * DK + d4);
+// acc += Σ_k A[r][k] B[r][k] with A a padded LDS tile (row stride lda floats)
+// and B an XOR-swizzled tile of CH 16-byte chunks per row starting at row b0
+// (b0 % 16 == 0); lane (r, g) covers k in [g·KLEN/4, (g + 1)·KLEN/4).
+template <int KLEN, int CH>
+__device__ __forceinline__ f4 nt_tile_swz(const float* A, int lda, const float* B, int b0, int r, int g, f4 acc) {
+  constexpr int P = KLEN / 4, Q = P / 4;
+  f4 a[Q], b[Q];
+  const float* pa = A + r * lda + g * P;
+  const float* pb = B + (b0 + r) * CH * 4;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    a[q] = *(const f4*)(pa + 4 * q);
+    b[q] = *(const f4*)(pb + 4 * ((g * Q + q) ^ r));
   }
-  // thread tid moves float4 number e = tid + 512 n of each 64 × 128 tile: row e / 32, columns 4 (e % 32)
-  auto fetch = [&](uint32_t c, ScanPrefetch& pf) {
-    const float* in = ws + ((size_t)c * NV + h) * kWsStride;
-    const uint32_t t0 = c * C;
+  __builtin_amdgcn_sched_barrier(0);
+  f4 acc2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int e = tid + kScanThreads * n, i = e >> 5, d4 = (e & 31) * 4;
-      pf.w[n] = *(const f4*)(in + kOffW + i * DK + d4);
-      const uint32_t t = min(t0 + i, T - 1);  // rows past T: any finite row (their W, U, M rows are 0)
-      pf.q[n] = *(const f4*)(q + ((size_t)t * NK + hk) * DK + d4);
-      pf.k[n] = t0 + i < T ? *(const f4*)(k + ((size_t)t * NK + hk) * DK + d4) : f4{0.f, 0.f, 0.f, 0.f};
-    }
+  for (int q = 0; q < Q; ++q)
 #pragma unroll
-    for (int n = 0; n < 2; ++n) pf.m[n] = *(const f4*)(in + kOffM + (tid + kScanThreads * n) * 4);
-    pf.u = *(const f4*)(in + kOffU + (tid >> 3) * DK + dv0 + (tid & 7) * 4);
-    pf.gam = tid < C ? in[kOffGam + tid] : 0.f;
-    pf.rho = tid < C ? in[kOffRho + tid] : 0.f;
-  };
-  auto stage = [&](const ScanPrefetch& pf) {
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int e = tid + kScanThreads * n, i = e >> 5, d4 = (e & 31) * 4;
-      *(f4*)(Ws + i * LDF + d4) = pf.w[n];
-      *(f4*)(Qs + i * LDF + d4) = pf.q[n];
-      *(f4*)(Ks + i * LDK + d4) = pf.k[n];
+    for (int e = 0; e < 4; e += 2) {
+      acc = mfma4(a[q][e], b[q][e], acc);
+      acc2 = mfma4(a[q][e + 1], b[q][e + 1], acc2);
     }
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int e = (tid + kScanThreads * n) * 4, i = e >> 6, j = e & 63;
-      *(f4*)(Ms + i * LDM + j) = pf.m[n];
-    }
-    *(f4*)(Us + (tid >> 3) * LDV2 + (tid & 7) * 4) = pf.u;
-    if (tid < C) {
-      Gm[tid] = pf.gam;
-      Rh[tid] = pf.rho;
-    }
-  };
+  return acc + acc2;
+}
 
+__global__ __launch_bounds__(320) void delta_chunk_scan_kernel(float* __restrict__ ws, const float* state_in,
+                                                               float* state_out, uint32_t T, uint32_t write_state) {
+  __shared__ __attribute__((aligned(16))) float Ss[kScanRows * LDF];
+  __shared__ __attribute__((aligned(1024))) float Wb[2][C * DK];   // [64 tokens][32 chunks], swizzled
+  __shared__ __attribute__((aligned(1024))) float Kb[2][DK * C];   // [128 keys][16 chunks], swizzled
+  __shared__ __attribute__((aligned(1024))) float Ub[2][C * kScanRows];  // [64 tokens][16 values]
+  __shared__ __attribute__((aligned(16))) float Vt[kScanRows * LDT];
+  __shared__ float Gc[2];
+  const uint32_t h = blockIdx.x, dv0 = blockIdx.y * kScanRows;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
   const uint32_t nch = (T + C - 1) / C;
-  ScanPrefetch pf;
-  fetch(0, pf);
-  for (uint32_t c = 0; c < nch; ++c) {
-    const uint32_t t0 = c * C;
-    __syncthreads();  // the previous chunk's reads of the staged tiles are done
-    stage(pf);
-    __syncthreads();
-    if (c + 1 < nch) fetch(c + 1, pf);  // in flight while this chunk computes
+  auto slot = [&](uint32_t c) { return ws + ((size_t)c * NV + h) * kWsStride; };
 
-    // V'ᵀ[dv][i] = Uᵀ − S Wᵀ on (value tile u, token tile i0)
-    {
-      f4 a0 = f4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
-#pragma unroll 8
-      for (int kk = 0; kk < DK; kk += 8) {
-        a0 = mfma4(Ss[(16 * u + r16) * LDF + kk + g4], Ws[(i0 + r16) * LDF + kk + g4], a0);
-        a1 = mfma4(Ss[(16 * u + r16) * LDF + kk + 4 + g4], Ws[(i0 + r16) * LDF + kk + 4 + g4], a1);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int at = (i0 + r16) * LDV2 + 16 * u + 4 * g4 + e;
-        Vp[at] = Us[at] - (a0[e] + a1[e]);
-      }
-    }
-    __syncthreads();
-    // Oᵀ[dv][i] = γ_i (S Qᵀ)[dv][i] + (V'ᵀ Mᵀ)[dv][i]; M is lower triangular, so tokens j < i0 + 16 only
-    {
-      f4 a0 = f4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
-#pragma unroll 8
-      for (int kk = 0; kk < DK; kk += 8) {
-        a0 = mfma4(Ss[(16 * u + r16) * LDF + kk + g4], Qs[(i0 + r16) * LDF + kk + g4], a0);
-        a1 = mfma4(Ss[(16 * u + r16) * LDF + kk + 4 + g4], Qs[(i0 + r16) * LDF + kk + 4 + g4], a1);
-      }
-      f4 acc = (a0 + a1) * Gm[i0 + r16];
-      for (int jj = 0; jj < i0 + 16; jj += 4)
-        acc = mfma4(Vp[(jj + g4) * LDV2 + 16 * u + r16], Ms[(i0 + r16) * LDM + jj + g4], acc);
-      const uint32_t t = t0 + i0 + r16;
-      if (t < T) {
-        float* dst = o + ((size_t)t * NV + h) * DV + dv0 + 16 * u + 4 * g4;  // o need only be 4-byte aligned
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[e] = acc[e];
-      }
-    }
-    // S ← γ_C S + V'ᵀ diag(γ_C/γ) K on (value tile u, key tiles 2 (w / 2) + {0, 1})
-    f4 sn[2];
-    const float gC = Gm[C - 1];
-#pragma unroll
-    for (int q2 = 0; q2 < 2; ++q2) {
-      const int d0 = 16 * (2 * (wave >> 1) + q2);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sn[q2][e] = gC * Ss[(16 * u + 4 * g4 + e) * LDF + d0 + r16];
+  // wave 4: chunk c's W, K̃ᵀ and U slice into buffer bf by DMA
+  auto dma_chunk = [&](uint32_t c, int bf) {
+    const float* in = slot(c);
+    const uint32_t wl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Wb[bf];
+    const uint32_t kl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Kb[bf];
+    const uint32_t ul = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Ub[bf];
 #pragma unroll 4
-      for (int jj = 0; jj < C; jj += 4) {
-        const int j = jj + g4;
-        sn[q2] = mfma4(Vp[j * LDV2 + 16 * u + r16], Ks[j * LDK + d0 + r16] * Rh[j], sn[q2]);
-      }
+    for (int n = 0; n < 32; ++n) {  // W: LDS chunk 64 n + lane = row 2 n + lane / 32, slot lane % 32
+      const int row = 2 * n + (lane >> 5), c4 = (lane & 31) ^ (row & 15);
+      dma16_lds(wl + n * 1024, (uint32_t)((row * DK + 4 * c4) * 4), in + kOffW);
     }
-    __syncthreads();  // every wave is done reading S
+#pragma unroll 4
+    for (int n = 0; n < 32; ++n) {  // K̃ᵀ: row 4 n + lane / 16, slot lane % 16
+      const int row = 4 * n + (lane >> 4), c4 = (lane & 15) ^ (row & 15);
+      dma16_lds(kl + n * 1024, (uint32_t)((row * C + 4 * c4) * 4), in + kOffKt);
+    }
 #pragma unroll
-    for (int q2 = 0; q2 < 2; ++q2) {
-      const int d0 = 16 * (2 * (wave >> 1) + q2);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Ss[(16 * u + 4 * g4 + e) * LDF + d0 + r16] = sn[q2][e];
+    for (int n = 0; n < 4; ++n) {  // U rows, columns dv0 .. + 16: row 16 n + lane / 4, chunk lane % 4
+      const int row = 16 * n + (lane >> 2);
+      dma16_lds(ul + n * 1024, (uint32_t)((row * DK + dv0 + 4 * (lane & 3)) * 4), in + kOffU);
+    }
+  };
+
+  if (wave == 4) {
+    dma_chunk(0, 0);
+    const float gc = slot(0)[kOffGam + C - 1];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) Gc[0] = gc;
+  } else {
+    for (int e = tid; e < kScanRows * DK / 4; e += 256) {
+      const int row = e >> 5, d4 = (e & 31) * 4;
+      *(f4*)(Ss + row * LDF + d4) = *(const f4*)(state_in + ((size_t)h * DV + dv0 + row) * DK + d4);
     }
   }
   __syncthreads();
-  if (write_state) {
-    for (int e = tid; e < kScanRows * DK / 4; e += kScanThreads) {
-      const int r = e >> 5, d4 = (e & 31) * 4;
-      *(f4*)(state_out + ((size_t)h * DV + dv0 + r) * DK + d4) = *(const f4*)(Ss + r * LDF + d4);
+
+  for (uint32_t c = 0; c < nch; ++c) {
+    const int bf = c & 1;
+    float* io = slot(c);
+    float gc_next = 0.f;
+    if (wave == 4) {
+      if (c + 1 < nch) {
+        dma_chunk(c + 1, bf ^ 1);  // buffer bf ^ 1 was last read during chunk c - 1
+        gc_next = slot(c + 1)[kOffGam + C - 1];
+      }
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {  // the chunk's starting S slice, for `out`
+        const int idx = 64 * n + lane, row = idx >> 5, c4 = idx & 31;
+        *(f4*)(io + kOffS + (dv0 + row) * DK + 4 * c4) = *(const f4*)(Ss + row * LDF + 4 * c4);
+      }
+    } else {  // V'ᵀ[dv][i] = U[i][dv] − Σ_d S[dv][d] W[i][d]
+      const int i0 = 16 * wave;
+      const f4 acc = nt_tile_swz<DK, 32>(Ss, LDF, Wb[bf], i0, r, g, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int dv = 4 * g + e, i = i0 + r;
+        Vt[dv * LDT + i] = Ub[bf][i * kScanRows + dv] - acc[e];
+      }
+    }
+    __syncthreads();  // V'ᵀ complete; every read of S for V' done
+    if (wave == 4) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {  // V'ᵀ, for `out`
+        const int idx = 64 * n + lane, row = idx >> 4, c4 = idx & 15;
+        *(f4*)(io + kOffVt + (dv0 + row) * C + 4 * c4) = *(const f4*)(Vt + row * LDT + 4 * c4);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next chunk's tiles have landed
+      if (lane == 0 && c + 1 < nch) Gc[bf ^ 1] = gc_next;
+    } else {  // S[dv][d] ← γ_C S[dv][d] + Σ_j V'ᵀ[dv][j] K̃ᵀ[d][j]; each wave reads and writes only its own columns
+      const float gC = Gc[bf];
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) {
+        const int d0 = 16 * (2 * wave + q2);
+        f4 acc;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = gC * Ss[(4 * g + e) * LDF + d0 + r];
+        acc = nt_tile_swz<C, 16>(Vt, LDT, Kb[bf], d0, r, g, acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Ss[(4 * g + e) * LDF + d0 + r] = acc[e];
+      }
+    }
+    __syncthreads();  // S and the next chunk's tiles are in place
+  }
+  if (write_state && wave < 4) {
+    for (int e = tid; e < kScanRows * DK / 4; e += 256) {
+      const int row = e >> 5, d4 = (e & 31) * 4;
+      *(f4*)(state_out + ((size_t)h * DV + dv0 + row) * DK + d4) = *(const f4*)(Ss + row * LDF + d4);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out: one workgroup per (chunk, value head, 32 value columns):
+//   O[i][dv] = γ_i Σ_d Q[i][d] S[dv][d] + Σ_{j ≤ i} M[i][j] V'ᵀ[dv][j]
+// Wave w owns tokens 16 w .. + 16 and loads its own operand rows (Q and M)
+// straight into registers in the MFMA's k layout; only the shared S and V'
+// columns go through LDS (26 KB), so several workgroups share a CU. M is
+// lower triangular: wave w sums token blocks jb ≤ w only.
+constexpr int kOutCols = 32;
+
+__global__ __launch_bounds__(256) void delta_chunk_out_kernel(const float* __restrict__ q,
+                                                              const float* __restrict__ ws, float* __restrict__ o,
+                                                              uint32_t T) {
+  __shared__ __attribute__((aligned(16))) float Sq[kOutCols * LDF];
+  __shared__ __attribute__((aligned(16))) float Vq[kOutCols * LDT];
+  const uint32_t c = blockIdx.x, h = blockIdx.y, hk = h >> 1, dv0 = blockIdx.z * kOutCols, t0 = c * C;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int i0 = 16 * wave;
+  const float* in = ws + ((size_t)c * NV + h) * kWsStride;
+  // this wave's operands: Q[i0 + r][32 g .. + 32] and M[i0 + r][16 jb + 4 g .. + 4], γ of its rows
+  f4 qa[8], ma[4];
+  {
+    const uint32_t t = t0 + i0 + r;
+    const float* qr = q + ((size_t)min(t, T - 1) * NK + hk) * DK + 32 * g;  // rows past T: any finite row
+#pragma unroll
+    for (int n = 0; n < 8; ++n) qa[n] = *(const f4*)(qr + 4 * n);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+      ma[jb] = jb <= wave ? *(const f4*)(in + kOffM + (i0 + r) * C + 16 * jb + 4 * g) : f4{0.f, 0.f, 0.f, 0.f};
+  }
+  f4 gi;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) gi[e] = in[kOffGam + i0 + 4 * g + e];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int e = (tid + 256 * n) * 4;
+    *(f4*)(Sq + (e >> 7) * LDF + (e & 127)) = *(const f4*)(in + kOffS + (dv0 + (e >> 7)) * DK + (e & 127));
+  }
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int e = (tid + 256 * n) * 4;
+    *(f4*)(Vq + (e >> 6) * LDT + (e & 63)) = *(const f4*)(in + kOffVt + (dv0 + (e >> 6)) * C + (e & 63));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int dt = 0; dt < kOutCols / 16; ++dt) {
+    f4 sb[8], vb[4];
+    const float* sr = Sq + (16 * dt + r) * LDF + 32 * g;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) sb[n] = *(const f4*)(sr + 4 * n);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) vb[jb] = *(const f4*)(Vq + (16 * dt + r) * LDT + 16 * jb + 4 * g);
+    __builtin_amdgcn_sched_barrier(0);
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = mfma4(qa[n][e], sb[n][e], acc);
+    acc *= gi;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      if (jb <= wave) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma4(ma[jb][s], vb[jb][s], acc);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t t = t0 + i0 + 4 * g + e;
+      if (t < T) o[((size_t)t * NV + h) * DV + dv0 + 16 * dt + r] = acc[e];
     }
   }
 }
@@ -380,8 +531,9 @@ hipError_t launch_gated_delta_chunked(const float* q, const float* k, const floa
   const uint32_t nch = (t + C - 1) / C;
   hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(nch, NV), dim3(256), 0, s, q, k, v, a, b, ldab, a_log, dt_bias, ws,
                      t);
-  hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(kScanThreads), 0, s, q, k, ws, state_in, state_out, o, t,
+  hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(320), 0, s, ws, state_in, state_out, t,
                      write_state ? 1u : 0u);
+  hipLaunchKernelGGL(delta_chunk_out_kernel, dim3(nch, NV, DV / kOutCols), dim3(256), 0, s, q, ws, o, t);
   return hipGetLastError();
 }
 

@@ -244,11 +244,12 @@ def main():
     ap.add_argument("--tokens", type=int, default=2307)
     ap.add_argument("--runs", type=int, default=5)
     ap.add_argument("--no-prune", action="store_true")
-    ap.add_argument("--delta-chunked", action="store_true", help="chunked gated delta recurrence (DH_DELTA_CHUNKED)")
+    ap.add_argument("--delta", choices=["auto", "chunked", "sequential"], default="auto",
+                    help="gated delta implementation (auto: chunked from DH_DELTA_CHUNK_MIN_T tokens)")
     args = ap.parse_args()
     if not hip.available():
         raise SystemExit("no GPU")
-    k = Kernels(delta_chunked=args.delta_chunked)
+    k = Kernels(delta=args.delta)
     st = Stream()
     s = st.handle
     t = args.tokens
@@ -269,7 +270,7 @@ def main():
         e1.synchronize()
         if i:
             times.append(e0.elapsed_ms(e1))
-    print(json.dumps({"layers": args.layers, "tokens": t, "runs": args.runs, "delta_chunked": args.delta_chunked,
+    print(json.dumps({"layers": args.layers, "tokens": t, "runs": args.runs, "delta": args.delta,
                       "p50_ms": float(np.median(times)),
                       "logits": logits.numpy().round(4).tolist()}), flush=True)
     model.close()

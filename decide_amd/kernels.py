@@ -64,12 +64,12 @@ def _call(rc: int) -> None:
 class Context:
     """One library context (the analog of the pipelines ``Kernels::new`` builds)."""
 
-    def __init__(self, imp: GemmImpl = GemmImpl.Fast, delta_chunked: bool = False):
+    def __init__(self, imp: GemmImpl = GemmImpl.Fast, delta: str = "auto"):
         lib = _lib.load()
         h = ctypes.c_void_p()
         flags = _lib.DH_GEMM_REFERENCE if imp == GemmImpl.Baseline else 0
-        if delta_chunked:  # the recurrence's other implementation (decide's DECIDE_DELTA, kernels/delta.rs:36-49)
-            flags |= _lib.DH_DELTA_CHUNKED
+        # the recurrence's implementation (decide's DECIDE_DELTA, kernels/delta.rs:36-49): "auto" picks by T
+        flags |= {"auto": 0, "chunked": _lib.DH_DELTA_CHUNKED, "sequential": _lib.DH_DELTA_SEQUENTIAL}[delta]
         _lib.check(lib.dh_ctx_create(flags, ctypes.byref(h)))
         self.handle = h
         self.imp = imp
@@ -294,8 +294,8 @@ def fill_normal_f16(ctx: Context, stream: int, out: Arg, n: int, seed: int, std:
 class Kernels:
     """decide's ``Kernels`` registry (kernels/mod.rs:40-67): the GEMM path and the forward kernels beside it."""
 
-    def __init__(self, imp: GemmImpl = GemmImpl.Fast, delta_chunked: bool = False):
-        self.ctx = Context(imp, delta_chunked)
+    def __init__(self, imp: GemmImpl = GemmImpl.Fast, delta: str = "auto"):
+        self.ctx = Context(imp, delta)
         self.gemm = Gemm(self.ctx)
         self.head = Head(self.ctx)
         self.norm = Norm(self.ctx)

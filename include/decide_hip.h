@@ -47,8 +47,11 @@ extern "C" {
 /* dh_ctx_create flags. */
 #define DH_GEMM_REFERENCE 1u /* every GEMM runs the simple M-independent kernel (decide's
                                 DECIDE_GEMM=baseline, kernels/gemm.rs:56-65) */
-#define DH_DELTA_CHUNKED 2u /* dh_gated_delta runs the chunked recurrence instead of the token-by-token
-                               kernel (the choice decide makes with DECIDE_DELTA, kernels/delta.rs:36-49) */
+#define DH_DELTA_CHUNKED 2u    /* dh_gated_delta always runs the chunked recurrence */
+#define DH_DELTA_SEQUENTIAL 4u /* dh_gated_delta always runs the token-by-token kernel (with neither flag:
+                                  chunked for t >= DH_DELTA_CHUNK_MIN_T, token by token below; the choice
+                                  decide makes with DECIDE_DELTA, kernels/delta.rs:36-49) */
+#define DH_DELTA_CHUNK_MIN_T 320u
 
 typedef struct dh_ctx dh_ctx;
 
@@ -202,10 +205,11 @@ int dh_conv_state_update(dh_ctx* ctx, void* stream, const float* p, const float*
  * a, b rows of stride ldab (value head h at column h); a_log, dt_bias [32];
  * state [32][128 dv][128 dk]. state_in may be state_out; with write_state 0
  * state_out is not written (and may be NULL). t >= 1, ldab >= 32; q, k and the
- * states 16-byte aligned. By default the recurrence runs token by token; a
- * context created with DH_DELTA_CHUNKED runs it 64 tokens at a time as fp32
- * matrix products, in a context workspace that dh_warm_up sizes for max_m
- * tokens. */
+ * states 16-byte aligned. From t = DH_DELTA_CHUNK_MIN_T on (or always, in a
+ * context created with DH_DELTA_CHUNKED) the recurrence runs 64 tokens at a
+ * time as fp32 matrix products, in a context workspace that dh_warm_up sizes
+ * for max_m tokens (a larger t grows it once); below that (or always, with
+ * DH_DELTA_SEQUENTIAL) it runs token by token. */
 int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, const float* v, const float* a,
                    const float* b, const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
                    float* o, uint32_t t, uint32_t ldab, uint32_t write_state);

@@ -51,9 +51,19 @@ def stream(gpu):
 
 @pytest.fixture(scope="session")
 def kernels_delta_chunked(gpu):
-    """A context whose gated delta runs the chunked recurrence."""
+    """A context whose gated delta always runs the chunked recurrence."""
     from decide_amd.kernels import Kernels
 
-    k = Kernels(delta_chunked=True)
+    k = Kernels(delta="chunked")
+    yield k
+    k.ctx.close()
+
+
+@pytest.fixture(scope="session")
+def kernels_delta_sequential(gpu):
+    """A context whose gated delta always runs the token-by-token kernel."""
+    from decide_amd.kernels import Kernels
+
+    k = Kernels(delta="sequential")
     yield k
     k.ctx.close()

@@ -137,3 +137,20 @@ def test_captured_forward_replays_match_eager(gpu, kernels):
     graph.close()
     st.destroy()
     model.close()
+
+
+def test_forward_delta_implementations_agree(gpu, kernels, kernels_delta_sequential):
+    """From DH_DELTA_CHUNK_MIN_T tokens on the default context runs the chunked recurrence; the same model
+    forward with the token-by-token kernel agrees within the parity tolerance (both are pinned against the
+    oracle's recurrence in test_mixer_gpu.py)."""
+    cfg = ModelConfig(layers=4, vocab=800, max_tokens=400, max_answers=3, max_cand=5)
+    ids, ans, cand, ncand = _request(400, cfg.vocab, 3, cfg.max_cand, 440)
+    out = []
+    for k in (kernels, kernels_delta_sequential):
+        model = Model(k.ctx, cfg)
+        model.init_random(0, seed=93)
+        out.append(_run(model, k, ids, ans, cand, ncand, cfg.max_cand, True))
+        model.close()
+    w = ~np.isnan(out[0])
+    assert np.array_equal(w, ~np.isnan(out[1]))
+    assert np.abs(out[0][w] - out[1][w]).max() <= MAX_LOGIT_DIFF

@@ -91,9 +91,9 @@ def _run_delta(kernels, stream, q, k, v, p, a_log, dt_bias, s0, t, in_place=Fals
 
 @pytest.mark.parametrize("t", [1, 5, 64, 70, 200, 1000])
 @pytest.mark.parametrize("impl", ["chunked", "sequential"])
-def test_gated_delta_matches_oracle(gpu, kernels, kernels_delta_chunked, stream, t, impl):
+def test_gated_delta_matches_oracle(gpu, kernels_delta_sequential, kernels_delta_chunked, stream, t, impl):
     q, k, v, p, a_log, dt_bias, s0 = _delta_inputs(t, 130)
-    ks = kernels_delta_chunked if impl == "chunked" else kernels
+    ks = kernels_delta_chunked if impl == "chunked" else kernels_delta_sequential
     o, s1 = _run_delta(ks, stream, q, k, v, p, a_log, dt_bias, s0, t)
     wo, ws = orc.gated_delta(q, k, v, p[:, LIN_A:LIN_A + NV], p[:, LIN_B:LIN_B + NV], a_log, dt_bias, s0, t)
     assert orc.rel_frobenius(o, wo) <= 1e-4, orc.rel_frobenius(o, wo)  # fp32 state vs f64 dots
@@ -101,10 +101,10 @@ def test_gated_delta_matches_oracle(gpu, kernels, kernels_delta_chunked, stream,
 
 
 @pytest.mark.parametrize("impl", ["chunked", "sequential"])
-def test_gated_delta_renormalises_a_fast_decay(gpu, kernels, kernels_delta_chunked, stream, impl):
+def test_gated_delta_renormalises_a_fast_decay(gpu, kernels_delta_sequential, kernels_delta_chunked, stream, impl):
     """g ≈ e^-37 per token: the sequential kernel's running scale drops below 2^-60 within two tokens,
     the chunked kernel's within-chunk ratios γ_i/γ_j underflow to 0."""
-    kernels = kernels_delta_chunked if impl == "chunked" else kernels
+    kernels = kernels_delta_chunked if impl == "chunked" else kernels_delta_sequential
     t = 12
     q, k, v, p, a_log, dt_bias, s0 = _delta_inputs(t, 140, a_log_std=0.0, a_shift=0.0)
     a_log[:] = 2.0
@@ -118,8 +118,8 @@ def test_gated_delta_renormalises_a_fast_decay(gpu, kernels, kernels_delta_chunk
 
 
 @pytest.mark.parametrize("impl", ["chunked", "sequential"])
-def test_gated_delta_in_place_chunks_and_no_write(gpu, kernels, kernels_delta_chunked, stream, impl):
-    kernels = kernels_delta_chunked if impl == "chunked" else kernels
+def test_gated_delta_in_place_chunks_and_no_write(gpu, kernels_delta_sequential, kernels_delta_chunked, stream, impl):
+    kernels = kernels_delta_chunked if impl == "chunked" else kernels_delta_sequential
     t1, t2 = 40, 30
     q, k, v, p, a_log, dt_bias, s0 = _delta_inputs(t1 + t2, 150)
     whole_o, whole_s = _run_delta(kernels, stream, q, k, v, p, a_log, dt_bias, s0, t1 + t2)
