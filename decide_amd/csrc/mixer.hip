@@ -48,41 +48,62 @@ __device__ __forceinline__ float row16_sum(float v) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// conv + SiLU + L2. One wave per (slot, row): slots 0-15 are q heads, 16-31 k
-// heads, 32-63 v heads (128 channels each); lane l owns channels 2l, 2l + 1
-// of the slot. Raw rows before the chunk come from `prev` [3][CONV_DIM].
-__global__ __launch_bounds__(64) void conv_silu_l2_kernel(const float* __restrict__ p, const float* __restrict__ prev,
-                                                          const float* __restrict__ w, float* __restrict__ q,
-                                                          float* __restrict__ k, float* __restrict__ v, uint32_t ldp) {
-  const uint32_t slot = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+// conv + SiLU + L2. One wave per (slot, run of 16 rows): slots 0-15 are q
+// heads, 16-31 k heads, 32-63 v heads (128 channels each); lane l owns
+// channels 2l, 2l + 1 of the slot. The wave loads the run's 16 rows and the 3
+// before it once (raw rows before the chunk come from `prev` [3][CONV_DIM]),
+// all loads in flight together, and slides the 4-tap window over them; each
+// output is the same fma chain as a single-row evaluation. Grid: (64 slots,
+// runs of 64 rows), 4 waves per workgroup each taking 16 of them.
+constexpr int kConvRun = 16;
+
+__global__ __launch_bounds__(256) void conv_silu_l2_kernel(const float* __restrict__ p, const float* __restrict__ prev,
+                                                           const float* __restrict__ w, float* __restrict__ q,
+                                                           float* __restrict__ k, float* __restrict__ v, uint32_t T,
+                                                           uint32_t ldp) {
+  const uint32_t slot = blockIdx.x, lane = threadIdx.x & 63;
+  const uint32_t t0 = blockIdx.y * 64 + (threadIdx.x >> 6) * kConvRun;
+  if (t0 >= T) return;
   const uint32_t c = slot * 128 + 2 * lane;  // slots are laid out q | k | v along the qkv columns
   const f4 w0 = *(const f4*)(w + (size_t)c * 4), w1 = *(const f4*)(w + (size_t)(c + 1) * 4);
-  float a0 = 0.f, a1 = 0.f;
+  f2 x[kConvRun + 3];  // raw rows t0 - 3 .. t0 + 15
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int s = (int)t - 3 + j;
-    const f2 x = s >= 0 ? *(const f2*)(p + (size_t)s * ldp + c) : *(const f2*)(prev + (size_t)(3 + s) * CONV_DIM + c);
-    a0 = fmaf(w0[j], x[0], a0);
-    a1 = fmaf(w1[j], x[1], a1);
+  for (int j = 0; j < kConvRun + 3; ++j) {
+    const int s = (int)t0 - 3 + j;
+    if (s < 0)
+      x[j] = *(const f2*)(prev + (size_t)(3 + s) * CONV_DIM + c);
+    else
+      x[j] = (uint32_t)s < T ? *(const f2*)(p + (size_t)s * ldp + c) : f2{0.f, 0.f};
   }
-  const float y0 = silu_fast(a0), y1 = silu_fast(a1);
-  if (slot >= 32) {
-    *(f2*)(v + ((size_t)t * NV + (slot - 32)) * DV + 2 * lane) = f2{y0, y1};
-    return;
-  }
-  const float inv = rsqrtf(wave_sum(y0 * y0 + y1 * y1) + 1e-6f);
-  if (slot < 16) {
-    const float sc = inv * 0.08838834764831845f;  // DK^-1/2
-    *(f2*)(q + ((size_t)t * NK + slot) * DK + 2 * lane) = f2{y0 * sc, y1 * sc};
-  } else {
-    *(f2*)(k + ((size_t)t * NK + (slot - 16)) * DK + 2 * lane) = f2{y0 * inv, y1 * inv};
+#pragma unroll
+  for (int u = 0; u < kConvRun; ++u) {
+    const uint32_t t = t0 + u;
+    if (t >= T) break;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a0 = fmaf(w0[j], x[u + j][0], a0);
+      a1 = fmaf(w1[j], x[u + j][1], a1);
+    }
+    const float y0 = silu_fast(a0), y1 = silu_fast(a1);
+    if (slot >= 32) {
+      *(f2*)(v + ((size_t)t * NV + (slot - 32)) * DV + 2 * lane) = f2{y0, y1};
+      continue;
+    }
+    const float inv = rsqrtf(wave_sum(y0 * y0 + y1 * y1) + 1e-6f);
+    if (slot < 16) {
+      const float sc = inv * 0.08838834764831845f;  // DK^-1/2
+      *(f2*)(q + ((size_t)t * NK + slot) * DK + 2 * lane) = f2{y0 * sc, y1 * sc};
+    } else {
+      *(f2*)(k + ((size_t)t * NK + (slot - 16)) * DK + 2 * lane) = f2{y0 * inv, y1 * inv};
+    }
   }
 }
 
 hipError_t launch_conv_silu_l2(const float* p, const float* prev, const float* w, float* q, float* k, float* v,
                                uint32_t t, uint32_t ldp, hipStream_t s) {
   if (t == 0) return hipSuccess;
-  hipLaunchKernelGGL(conv_silu_l2_kernel, dim3(64, t), dim3(64), 0, s, p, prev, w, q, k, v, ldp);
+  hipLaunchKernelGGL(conv_silu_l2_kernel, dim3(64, (t + 63) / 64), dim3(256), 0, s, p, prev, w, q, k, v, t, ldp);
   return hipGetLastError();
 }
 
