@@ -5,8 +5,11 @@
 // the softmax weights rounded to fp16 once as the P·V operand, y fp16.
 //
 // Design (MI355X's own):
-//   * A workgroup is one kv head × 16 query rows; its 4 waves are the 4 query
-//     heads sharing that kv head, so one staged K/V tile serves all four.
+//   * A workgroup is one kv head × 32 query rows; its 8 waves are the 4 query
+//     heads sharing that kv head × 2 blocks of 16 rows, so one staged K/V tile
+//     serves all eight (the tiles come from L2 once per 32 rows, which is what
+//     bounds this kernel). The next block's K/V rows are loaded into registers
+//     while the current block computes.
 //   * Everything is computed transposed: Sᵀ = K·Qᵀ (A = K rows from LDS,
 //     B = the wave's Q rows held in registers for the whole kernel) and
 //     Oᵀ += Vᵀ·Pᵀ. In the MFMA output layout a lane then holds 8 scores of
@@ -35,7 +38,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kHD = 256, kNQ = 16, kQDim = kNQ * kHD;
-constexpr int kBQ = 16;    // query rows per workgroup
+constexpr int kBQ = 32;    // query rows per workgroup (2 blocks of 16)
 constexpr int kBKey = 32;  // keys per block
 constexpr int kKLD = kHD + 8;  // K tile row stride (halves): 528 B, conflict-free 16-lane reads
 constexpr int kVLD = kBKey + 8;  // Vᵀ tile row stride (halves): 80 B
@@ -47,23 +50,25 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
 }
 }  // namespace
 
-__global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ kc,
+__global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, const float* __restrict__ pq,
                                                         const uint32_t* __restrict__ qpos, _Float16* __restrict__ y,
                                                         uint32_t ldq, uint32_t rows) {
   __shared__ __attribute__((aligned(16))) _Float16 ks[kBKey * kKLD];
   __shared__ __attribute__((aligned(16))) _Float16 vts[kHD * kVLD];
+  __shared__ uint32_t wpmax[8];
   const uint32_t qb = gridDim.x - 1 - blockIdx.x;
   const uint32_t kvh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t h = kvh * 4 + wave;
+  const uint32_t h = kvh * 4 + (wave & 3);
   const int rl = lane & 15, g = lane >> 4;
-  const uint32_t r0 = qb * kBQ;
+  const uint32_t r0 = qb * kBQ + 16 * (wave >> 2);
   const uint32_t row = min(r0 + rl, rows - 1);
   const uint32_t mypos = qpos[row];
   uint32_t pmax = mypos;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) pmax = max(pmax, (uint32_t)__shfl_xor((int)pmax, o, 64));
+  if (lane == 0) wpmax[wave] = pmax;
 
   h8 qf[8];
 #pragma unroll
@@ -72,30 +77,38 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
 #pragma unroll
   for (int i = 0; i < 16; ++i) oacc[i] = f4{0.f, 0.f, 0.f, 0.f};
   float m = kNeg, lsum = 0.f;
+  __syncthreads();
+  // the workgroup's last key: the largest position over its 32 rows (loads past it are clamped to it)
+  uint32_t kmax = wpmax[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) kmax = max(kmax, wpmax[i]);
 
-  const uint32_t nblk = pmax / kBKey + 1;
-  const int kq = tid & 7, dc = tid >> 3;  // V staging: key quad, 8-dim chunk
+  const uint32_t nblk = kmax / kBKey + 1;
+  // staging: K rows as 16-byte chunks (thread → key id / 32, chunk id % 32, two per thread);
+  // V as key pairs × 8-dim chunks, transposed into vts on the way in
+  const int kp = tid & 15, dc = tid >> 4;
+  h8 kpre[2], vpre[2];
+  auto fetch = [&](uint32_t kb0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int id = tid + 512 * i, key = id >> 5, c16 = id & 31;
+      kpre[i] = *(const h8*)(kc + ((size_t)min(kb0 + key, kmax) * 4 + kvh) * kHD + 8 * c16);
+      vpre[i] = *(const h8*)(vc + ((size_t)min(kb0 + 2 * kp + i, kmax) * 4 + kvh) * kHD + 8 * dc);
+    }
+  };
+  fetch(0);
   for (uint32_t blk = 0; blk < nblk; ++blk) {
     const uint32_t kb0 = blk * kBKey;
     __syncthreads();  // the previous block's LDS reads are done
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = tid + 256 * i, key = id >> 5, c16 = id & 31;
-      const uint32_t src = min(kb0 + key, pmax);
-      *(h8*)(ks + key * kKLD + 8 * c16) = *(const h8*)(kc + ((size_t)src * 4 + kvh) * kHD + 8 * c16);
+    for (int i = 0; i < 2; ++i) {
+      const int id = tid + 512 * i, key = id >> 5, c16 = id & 31;
+      *(h8*)(ks + key * kKLD + 8 * c16) = kpre[i];
     }
-    {
-      h8 vv[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t src = min(kb0 + 4 * kq + e, pmax);
-        vv[e] = *(const h8*)(vc + ((size_t)src * 4 + kvh) * kHD + 8 * dc);
-      }
-#pragma unroll
-      for (int d = 0; d < 8; ++d)
-        *(h4*)(vts + (8 * dc + d) * kVLD + 4 * kq) = h4{vv[0][d], vv[1][d], vv[2][d], vv[3][d]};
-    }
+    for (int d = 0; d < 8; ++d) *(h2*)(vts + (8 * dc + d) * kVLD + 2 * kp) = h2{vpre[0][d], vpre[1][d]};
     __syncthreads();
+    if (blk + 1 < nblk) fetch(kb0 + kBKey);  // in flight while this block computes
 
     f4 st[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -166,7 +179,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
 hipError_t launch_attention(const _Float16* q, const _Float16* kc, const _Float16* vc, const float* pq,
                             const uint32_t* qpos, _Float16* y, uint32_t rows, uint32_t ldq, hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(attention_kernel, dim3((rows + kBQ - 1) / kBQ, 4), dim3(256), 0, s, q, kc, vc, pq, qpos, y, ldq,
+  hipLaunchKernelGGL(attention_kernel, dim3((rows + kBQ - 1) / kBQ, 4), dim3(512), 0, s, q, kc, vc, pq, qpos, y, ldq,
                      rows);
   return hipGetLastError();
 }
