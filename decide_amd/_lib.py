@@ -20,6 +20,7 @@ DH_ENOMEM = 3
 DH_EDEVICE = 4
 
 DH_GEMM_REFERENCE = 1
+DH_GEMM_STREAM_VARIANT = 64
 DH_DELTA_CHUNKED = 2
 DH_DELTA_SEQUENTIAL = 4
 DH_DELTA_CHUNK_MIN_T = 320

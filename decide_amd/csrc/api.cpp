@@ -44,7 +44,9 @@ int hip_status(hipError_t e, const char* what) {
   return fail(DH_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
 }
 
-void mark(dh_ctx* c, int kid) { c->used.fetch_or(1ull << kid, std::memory_order_relaxed); }
+void mark(dh_ctx* c, int kid) {
+  if (kid >= 0 && kid < 64) c->used.fetch_or(1ull << kid, std::memory_order_relaxed);
+}
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -130,7 +132,8 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
   a.splits = p.splits;
   a.kps = p.kps;
   a.count = count;
-  const dh::VariantInfo vi = dh::variant_info(p.variant);
+  const bool stream = p.variant == dh::kStreamVariant;
+  const uint32_t bn = stream ? 32u : (uint32_t)dh::variant_info(p.variant).bn();
   uint32_t stripes = 0;
   for (uint32_t i = 0; i < count; ++i) {
     a.mem[i].w = (const _Float16*)mem[i].w;
@@ -140,7 +143,7 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
     a.mem[i].n = mem[i].n;
     a.mem[i].epi = mem[i].epi;
     a.mem[i].stripe_begin = stripes;
-    stripes += (mem[i].n + vi.bn() - 1) / vi.bn();
+    stripes += (mem[i].n + bn - 1) / bn;
   }
   a.nstripes = stripes;
   if (p.splits > 1) {
@@ -150,8 +153,14 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
     a.ws = c->ws;
   }
   const uint32_t grid = p.mtiles * stripes * p.splits;
-  mark(c, p.variant);
-  int rc = hip_status(dh::launch_tile(p.variant, a, grid, s), "gemm tile kernel launch");
+  int rc;
+  if (stream) {
+    mark(c, kKidStream);
+    rc = hip_status(dh::launch_stream(a, grid, s), "gemm streaming kernel launch");
+  } else {
+    mark(c, p.variant);
+    rc = hip_status(dh::launch_tile(p.variant, a, grid, s), "gemm tile kernel launch");
+  }
   if (rc != DH_OK || p.splits == 1) return rc;
   mark(c, kKidReduce);
   return hip_status(dh::launch_splitk_reduce(c->ws, p.splits, m, mem[0].n, mem[0].y, mem[0].ldy, mem[0].epi, s),
@@ -250,16 +259,24 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
   return launch_plan(ctx, s, p, x, ldx, m, k, members, count);
 }
 
+static_assert(dh::kStreamVariant == (int)DH_GEMM_STREAM_VARIANT, "the streaming kernel's plan id");
+
 int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint32_t epi, dh_gemm_plan* out) {
   if (!out) return fail(DH_EINVAL, "dh_gemm_plan_for: out is NULL");
   if (epi > 3u || m < 1 || n % 32 || k % 32) return fail(DH_EINVAL, "dh_gemm_plan_for: invalid shape");
   const dh::Plan p = choose_plan(ctx, m, n, k, epi);
   if (p.variant < 0) return fail(DH_EINVAL, "dh_gemm_plan_for: no plan");
-  const dh::VariantInfo vi = dh::variant_info(p.variant);
   out->variant = (uint32_t)p.variant;
-  out->bm = (uint32_t)vi.bm();
-  out->bn = (uint32_t)vi.bn();
-  out->waves = (uint32_t)vi.wn;
+  if (p.variant == dh::kStreamVariant) {
+    out->bm = dh::kStreamMaxM;
+    out->bn = 32;
+    out->waves = 4;
+  } else {
+    const dh::VariantInfo vi = dh::variant_info(p.variant);
+    out->bm = (uint32_t)vi.bm();
+    out->bn = (uint32_t)vi.bn();
+    out->waves = (uint32_t)vi.wn;
+  }
   out->splits = p.splits;
   out->workgroups = p.grid;
   out->ws_bytes = p.ws_bytes;
@@ -320,9 +337,10 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
     int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(std::max(1u, max_m)) * sizeof(float));
     if (rc != DH_OK) return rc;
   }
-  // One tiny launch of every tile variant (M = 16, N = bn, K = 64) into scratch.
+  // One tiny launch of every tile variant (M = 16, N = bn, K = 64) and of the
+  // streaming kernel (M = 16, N = 32, K = 128) into scratch.
   void* scratch = nullptr;
-  const size_t xb = 16 * 64 * 2, wb = 512 * 64 * 2, yb = 16 * 512 * 4;
+  const size_t xb = 16 * 128 * 2, wb = 512 * 64 * 2, yb = 16 * 512 * 4;
   hipError_t e = hipMalloc(&scratch, xb + wb + yb);
   if (e != hipSuccess) return fail(DH_ENOMEM, "dh_warm_up: %s", hipGetErrorString(e));
   e = hipMemsetAsync(scratch, 0, xb + wb + yb, s);
@@ -332,6 +350,10 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
     const dh::VariantInfo vi = dh::variant_info(v);
     dh_gemm_member mem{base + xb, base + xb + wb, 64, (uint32_t)vi.bn(), (uint32_t)vi.bn(), DH_EPI_STORE_F32};
     rc = launch_plan(ctx, s, dh::plan_make(v, 1, 16, vi.bn(), 64, 0u), base, 64, 16, 64, &mem, 1);
+  }
+  if (rc == DH_OK) {
+    dh_gemm_member mem{base + xb, base + xb + wb, 128, 32, 32, DH_EPI_STORE_F32};
+    rc = launch_plan(ctx, s, dh::plan_stream(16, 32, 128, 0), base, 128, 16, 128, &mem, 1);
   }
   if (rc == DH_OK && need) {
     // and the split-K reduction once (two splits of K = 128)

@@ -26,12 +26,15 @@ struct dh_ctx {
 
 namespace dh_api {
 
-// Kernel ids for dh_variants_loaded beyond the tile menu (ids < 48).
+// Kernel ids for dh_variants_loaded beyond the tile menu (ids < kMaxTileVariants);
+// every id is below 64, one bit of dh_ctx::used each.
+constexpr int kMaxTileVariants = 16;
 enum : int {
-  kKidReduce = 48, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
+  kKidReduce = kMaxTileVariants, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
   kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny,
-  kKidDeltaChunk
+  kKidDeltaChunk, kKidStream, kKidCount
 };
+static_assert(kKidCount <= 64, "kernel ids must fit dh_ctx::used");
 
 // Records `fmt` as the thread's last error and returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -43,6 +43,11 @@ struct VariantInfo {
   int bn() const { return 16 * fn * wn; }
 };
 
+// The small-M weight-streaming kernel (gemm_stream.hip) over the members of
+// `a`: a.nstripes counts 32-column blocks (mem[i].stripe_begin in those
+// units), a.kps is a multiple of 128, grid = a.nstripes · a.splits.
+hipError_t launch_stream(const TileArgs& a, uint32_t grid, hipStream_t s);
+
 int variant_count();
 VariantInfo variant_info(int v);
 // Enqueues the tile kernel of variant v over `grid` workgroups.

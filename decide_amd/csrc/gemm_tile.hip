@@ -528,6 +528,7 @@ struct VariantEntry {
 static const VariantEntry kVariants[] = {DH_TILE_MENU(DH_TILE_ENTRY)};
 #undef DH_TILE_ENTRY
 
+static_assert(sizeof(kVariants) / sizeof(kVariants[0]) <= 16, "the C ABI numbers other kernels from 16 on");
 int variant_count() { return (int)(sizeof(kVariants) / sizeof(kVariants[0])); }
 VariantInfo variant_info(int v) { return kVariants[v].info; }
 

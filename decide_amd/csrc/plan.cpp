@@ -216,7 +216,34 @@ Plan plan_model(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_w
 }
 }  // namespace
 
+// The weight-streaming kernel for M <= 16: one workgroup per 32 columns and
+// K split, splits chosen so that about two workgroups per CU stream at once
+// (each split a whole number of 128-wide k blocks; no split when the
+// workspace is capped, as for grouped launches).
+Plan plan_stream(uint32_t m, uint32_t n, uint32_t k, uint64_t max_ws) {
+  Plan p{};
+  p.variant = kStreamVariant;
+  const uint32_t blocks = n / 32, kb = k / 128;
+  uint32_t s = std::min(std::max(1u, ceil_div(512, blocks)), kb);
+  const uint32_t kpb = ceil_div(kb, s);
+  s = ceil_div(kb, kpb);
+  p.splits = s;
+  p.kps = kpb * 128;
+  p.ws_bytes = s > 1 ? (uint64_t)s * m * n * 4 : 0;
+  if (p.ws_bytes > max_ws) {
+    p.splits = 1;
+    p.kps = k;
+    p.ws_bytes = 0;
+  }
+  p.mtiles = 1;
+  p.stripes = blocks;
+  p.grid = blocks * p.splits;
+  p.est_us = (double)n * k * 2 / kHbmBps * 1e6 + kLaunchUs;
+  return p;
+}
+
 Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws) {
+  if (m <= kStreamMaxM && n <= kStreamMaxN && k % 128 == 0 && n % 32 == 0) return plan_stream(m, n, k, max_ws);
   const Measured* near = nullptr;
   double best_rel = 0.12;
   for (const Measured& e : kMeasured) {

@@ -21,11 +21,22 @@ struct Plan {
   double est_us;      // model estimate
 };
 
+// Plan.variant of the small-M weight-streaming kernel (gemm_stream.hip): 32
+// output columns per workgroup, M <= 16, K a multiple of 128.
+constexpr int kStreamVariant = 64;  // DH_GEMM_STREAM_VARIANT
+constexpr uint32_t kStreamMaxM = 16;
+// Widest N (summed over a grouped launch's members) the streaming kernel takes:
+// measured faster than the FM = 1/2 tile variants with split-K up to here
+// (k|v, o and down of the pruned layer) and slower beyond (q|gate, gate|up).
+constexpr uint32_t kStreamMaxN = 4096;
+
 // Model estimate for one (variant, splits) choice; +inf if the choice is not
 // valid for the shape.
 double plan_estimate_us(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
 // Builds the plan for (variant, splits), filling the derived fields.
 Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
+// The weight-streaming kernel's plan (M <= kStreamMaxM, K % 128 == 0, N % 32 == 0).
+Plan plan_stream(uint32_t m, uint32_t n, uint32_t k, uint64_t max_ws);
 // Best plan for a single GEMM. `max_ws` caps the split-K workspace bytes.
 Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws);
 // Best plan for a grouped launch of total width n_total (no split-K).

@@ -66,8 +66,11 @@ typedef struct dh_gemm_member {
 } dh_gemm_member;
 
 /* A launch plan as the planner chose it (for tests, tuning and reports). */
+#define DH_GEMM_STREAM_VARIANT 64u /* dh_gemm_plan.variant of the small-M weight-streaming kernel (M <= 16,
+                                      N <= 4096, K % 128 == 0; decide's gemm_nt_small, gemm_fast.metal:429-566): 16 × 32
+                                      output tiles, 4 waves, W streamed from HBM straight into registers */
 typedef struct dh_gemm_plan {
-  uint32_t variant;     /* index into the compiled tile-kernel menu */
+  uint32_t variant;     /* index into the compiled tile-kernel menu, or DH_GEMM_STREAM_VARIANT */
   uint32_t bm, bn;      /* output tile (rows, columns) */
   uint32_t waves;       /* wavefronts per workgroup */
   uint32_t splits;      /* split-K factor (1 = none) */

@@ -65,6 +65,53 @@ def test_small_shapes_planner(gpu, kernels, stream, m, n, k, epi):
     orc.assert_close(f"m{m} n{n} k{k} {epi.name}", got, want, atol=tol, rtol=tol)
 
 
+# the weight-streaming kernel (M <= 16, K % 128 == 0): split-K and single-pass shapes, ragged M, N tails
+STREAM = [(1, 32, 128), (3, 2560, 9216), (16, 4096, 2560), (7, 96, 384), (16, 64, 1024), (13, 2048, 2560),
+          (2, 160, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", STREAM)
+@pytest.mark.parametrize("epi", list(Epilogue))
+def test_weight_streaming_kernel(gpu, kernels, stream, m, n, k, epi):
+    from decide_amd import _lib
+
+    assert kernels.gemm.plan(m, n, k, epi)["variant"] == _lib.DH_GEMM_STREAM_VARIANT
+    x, w = inputs(m, n, k, 700 + m + n)
+    y0 = synth.normal_f32(synth.seed_for(98), (m, n), 1.0) if epi == Epilogue.AddF32 else None
+    got = run_gemm(kernels, stream, x, w, epi, y0)
+    want = oracle_epi(x, w, epi, y0)
+    check_gemm(f"stream m{m} n{n} k{k} {epi.name}", got, want)
+    tol = 2e-3 if epi in (Epilogue.StoreF16, Epilogue.SwigluF16) else 1e-4
+    orc.assert_close(f"stream m{m} n{n} k{k} {epi.name}", got, want, atol=tol, rtol=tol)
+    assert np.array_equal(got, run_gemm(kernels, stream, x, w, epi, y0)), "not deterministic"
+
+
+def test_weight_streaming_grouped(gpu, kernels, stream):
+    """A grouped launch of three members (SwiGLU, fp32 and fp16) at M = 3 on the streaming kernel."""
+    from decide_amd import _lib
+    from decide_amd.kernels import addr
+
+    m, k = 3, 2560
+    x = synth.normal_f16(synth.seed_for(801), (m, k), 1.0)
+    ws = [synth.normal_f16(synth.seed_for(802 + i), (n, k), 0.02) for i, n in enumerate((512, 224, 96))]
+    epis = [Epilogue.SwigluF16, Epilogue.StoreF32, Epilogue.StoreF16]
+    outs, members = [], []
+    for w, epi in zip(ws, epis):
+        cols = w.shape[0] // 2 if epi == Epilogue.SwigluF16 else w.shape[0]
+        y = full((m, cols), np.float32 if epi == Epilogue.StoreF32 else np.float16, np.nan)
+        wd = to_dev(w)
+        outs.append((y, wd))
+        members.append(_lib.DhGemmMember(addr((wd, 0)), addr((y, 0)), k, cols, w.shape[0], int(epi)))
+    arr = (_lib.DhGemmMember * 3)(*members)
+    xd = to_dev(x)
+    assert _lib.load().dh_gemm_nt_grouped(kernels.ctx.handle, None, addr((xd, 0)), k, m, k, arr, 3) == 0
+    sync()
+    for (y, _), w, epi in zip(outs, ws, epis):
+        got = to_host(y).astype(np.float32)
+        want = oracle_epi(x, w, epi)
+        check_gemm(f"grouped stream {epi.name}", got, want)
+
+
 @pytest.mark.parametrize("variant", range(len(variants())))
 def test_every_variant_and_split_on_integer_inputs_is_exact(gpu, kernels, stream, variant):
     """Integer-valued fp16 in [-4, 4] at K = 288 (4 full stages and a 32-wide tail): every partial
