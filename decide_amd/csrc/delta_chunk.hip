@@ -300,10 +300,13 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
 constexpr int kScanRows = 16;
 
 // 16 bytes per lane global → LDS: lane l's 16 bytes at sbase + voff land at
-// LDS byte address lds_byte + 16·l. M0 is written in the same statement (one
-// wait state before its use); nothing else in this file reads M0. Both the
-// LDS address and the base must be wave-uniform: they go through
-// readfirstlane into SGPRs.
+// LDS byte address lds_byte + 16·l. M0 is written in the same statement;
+// nothing else in this file reads M0. Both the LDS address and the base must
+// be wave-uniform: they go through readfirstlane into SGPRs. A VMEM
+// instruction may read an SGPR only 5 wait states after a VALU instruction
+// (the readfirstlane) wrote it; the compiler cannot see the load inside the
+// asm string, so the statement supplies them itself (s_mov + s_nop 4), which
+// also covers the one wait state between the M0 write and its use.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16_lds(uint32_t lds_byte, uint32_t voff, const void* sbase) {
@@ -311,7 +314,7 @@ __device__ __forceinline__ void dma16_lds(uint32_t lds_byte, uint32_t voff, cons
   const uint64_t ub = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
                       (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
   const uint32_t ul = __builtin_amdgcn_readfirstlane(lds_byte);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(ul), "v"(voff),
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(ul), "v"(voff),
                "s"((const void*)(uintptr_t)ub)
                : "memory", "m0");
 }

@@ -1,9 +1,14 @@
 // Measurement probe (not part of the library): how fast one CU can pull data
 // from L2 (or HBM) into LDS with global_load_lds_dwordx4, the DMA every GEMM
-// tile stage is fed by, as a function of the waves issuing it. One workgroup
-// per CU; each wave issues `depth` 1 KB DMAs, waits for them, and repeats
-// over its own window of a buffer that either fits L2 (2 MB, re-read) or
-// does not (1 GB, streamed from HBM).
+// tile stage is fed by, as a function of the waves issuing it, with plain
+// global_load_dwordx4 into registers beside it. One workgroup per CU; each
+// wave issues `depth` 1 KB loads, waits for them, and repeats over its own
+// window of a buffer that either fits L2 (2 MB, re-read) or does not (1 GB,
+// streamed from HBM). Both sizes are powers of two, so addresses wrap with a
+// mask: a 64-bit `%` here would compile to a software division per load and
+// measure that instead of the memory system. The DMA's base comes from
+// readfirstlane, so the asm statement supplies the 5 wait states a VMEM read
+// of a VALU-written SGPR needs (s_mov + s_nop 4).
 //
 // Build and run: make -C decide_amd/csrc probe && decide_amd/csrc/_build/l2_probe
 #include <hip/hip_runtime.h>
@@ -12,20 +17,28 @@
 
 #pragma clang diagnostic ignored "-Winline-asm"
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// byte offset of load n of iteration `it` for `wave`, wrapped into the window
 template <int DEPTH, int NT>
-__global__ __launch_bounds__(NT) void dma_probe_kernel(const char* __restrict__ g, size_t span, int iters, float* out) {
+__device__ __forceinline__ uint32_t probe_off(uint32_t base, int it, int wave, int n, uint32_t mask) {
+  return (base + (uint32_t)((it * (NT / 64) + wave) * DEPTH + n) * 1024u) & mask;
+}
+
+template <int DEPTH, int NT>
+__global__ __launch_bounds__(NT) void dma_probe_kernel(const char* __restrict__ g, uint32_t mask, int iters, float* out) {
   __shared__ __attribute__((aligned(1024))) char buf[64 * 1024];
   const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)buf;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const size_t base = ((size_t)blockIdx.x * 131072) % span;
+  const uint32_t base = (blockIdx.x * 131072u) & mask;
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int n = 0; n < DEPTH; ++n) {
       const uint32_t l = __builtin_amdgcn_readfirstlane(lds + (uint32_t)((wave * DEPTH + n) % 64) * 1024);
-      const uint64_t src = (uint64_t)(g + ((base + (size_t)(it * (NT / 64) * DEPTH + wave * DEPTH + n) * 1024) % span));
+      const uint64_t src = (uint64_t)(g + probe_off<DEPTH, NT>(base, it, wave, n, mask));
       const uint64_t s = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(src >> 32)) << 32) |
                          (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)src);
-      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(l),
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(l),
                    "v"((uint32_t)(lane * 16)), "s"((const void*)s)
                    : "memory", "m0");
     }
@@ -35,33 +48,59 @@ __global__ __launch_bounds__(NT) void dma_probe_kernel(const char* __restrict__ 
   if (threadIdx.x == 0) out[blockIdx.x] = ((float*)buf)[lane];
 }
 
+template <int DEPTH, int NT>
+__global__ __launch_bounds__(NT) void vgpr_probe_kernel(const char* __restrict__ g, uint32_t mask, int iters, float* out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t base = (blockIdx.x * 131072u) & mask;
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+    f4 x[DEPTH];
+#pragma unroll
+    for (int n = 0; n < DEPTH; ++n) {
+      const char* src = g + probe_off<DEPTH, NT>(base, it, wave, n, mask) + lane * 16;
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(x[n]) : "v"(src) : "memory");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int n = 0; n < DEPTH; ++n) {
+      asm volatile("" : "+v"(x[n]));  // after the wait: the loaded values are final here
+      acc += x[n];
+    }
+  }
+  if (acc[0] == 1234.5f) out[blockIdx.x] = acc[1];
+}
+
 int main() {
-  const size_t span_l2 = 2u << 20, span_hbm = 1024u << 20;
+  const uint32_t span_l2 = 2u << 20, span_hbm = 1024u << 20;
   char* g = nullptr;
   float* out = nullptr;
-  if (hipMalloc(&g, span_hbm + (1 << 20)) != hipSuccess || hipMalloc(&out, 4096 * 4) != hipSuccess) {
+  if (hipMalloc(&g, (size_t)span_hbm + (1 << 20)) != hipSuccess || hipMalloc(&out, 4096 * 4) != hipSuccess) {
     fprintf(stderr, "hipMalloc failed\n");
     return 1;
   }
-  (void)hipMemset(g, 1, span_hbm + (1 << 20));
+  (void)hipMemset(g, 1, (size_t)span_hbm + (1 << 20));
   hipEvent_t e0, e1;
   (void)hipEventCreate(&e0);
   (void)hipEventCreate(&e1);
   const int iters = 400, grid = 256;
   struct Case {
     const char* name;
-    void (*k)(const char*, size_t, int, float*);
+    void (*k)(const char*, uint32_t, int, float*);
     int depth, nt;
-  } cases[] = {{"4 waves x 16 KB", dma_probe_kernel<16, 256>, 16, 256},
-               {"4 waves x 32 KB", dma_probe_kernel<32, 256>, 32, 256},
-               {"8 waves x 16 KB", dma_probe_kernel<16, 512>, 16, 512},
-               {"16 waves x 8 KB", dma_probe_kernel<8, 1024>, 8, 1024}};
-  printf("| waves per CU x bytes in flight per wave | source | GB/s per CU | GB/s total (256 CUs) |\n|---|---|---|---|\n");
+  } cases[] = {{"DMA, 4 waves x 8 KB", dma_probe_kernel<8, 256>, 8, 256},
+               {"DMA, 4 waves x 16 KB", dma_probe_kernel<16, 256>, 16, 256},
+               {"DMA, 4 waves x 32 KB", dma_probe_kernel<32, 256>, 32, 256},
+               {"DMA, 8 waves x 16 KB", dma_probe_kernel<16, 512>, 16, 512},
+               {"DMA, 16 waves x 8 KB", dma_probe_kernel<8, 1024>, 8, 1024},
+               {"VGPR, 4 waves x 16 KB", vgpr_probe_kernel<16, 256>, 16, 256},
+               {"VGPR, 8 waves x 16 KB", vgpr_probe_kernel<16, 512>, 16, 512}};
+  printf("| loads, waves per CU x bytes in flight per wave | source | GB/s per CU | GB/s total (256 CUs) |\n");
+  printf("|---|---|---|---|\n");
   for (const Case& c : cases)
-    for (size_t span : {span_l2, span_hbm}) {
-      for (int w = 0; w < 3; ++w) hipLaunchKernelGGL(c.k, dim3(grid), dim3(c.nt), 0, 0, g, span, iters, out);
+    for (uint32_t span : {span_l2, span_hbm}) {
+      for (int w = 0; w < 3; ++w) hipLaunchKernelGGL(c.k, dim3(grid), dim3(c.nt), 0, 0, g, span - 1, iters, out);
       (void)hipEventRecord(e0);
-      hipLaunchKernelGGL(c.k, dim3(grid), dim3(c.nt), 0, 0, g, span, iters, out);
+      hipLaunchKernelGGL(c.k, dim3(grid), dim3(c.nt), 0, 0, g, span - 1, iters, out);
       (void)hipEventRecord(e1);
       if (hipEventSynchronize(e1) != hipSuccess) {
         fprintf(stderr, "kernel failed\n");
