@@ -275,7 +275,7 @@ int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint
     const dh::VariantInfo vi = dh::variant_info(p.variant);
     out->bm = (uint32_t)vi.bm();
     out->bn = (uint32_t)vi.bn();
-    out->waves = (uint32_t)vi.wn;
+    out->waves = (uint32_t)vi.waves();
   }
   out->splits = p.splits;
   out->workgroups = p.grid;
@@ -305,7 +305,7 @@ int dh_gemm_variant_info(uint32_t variant, uint32_t* bm, uint32_t* bn, uint32_t*
   const dh::VariantInfo vi = dh::variant_info((int)variant);
   if (bm) *bm = (uint32_t)vi.bm();
   if (bn) *bn = (uint32_t)vi.bn();
-  if (waves) *waves = (uint32_t)vi.wn;
+  if (waves) *waves = (uint32_t)vi.waves();
   if (wave_cols) *wave_cols = (uint32_t)(16 * vi.fn);
   return ok();
 }

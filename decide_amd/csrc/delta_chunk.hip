@@ -299,24 +299,36 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
 // conflict-free.
 constexpr int kScanRows = 16;
 
+// Wave-uniform copies in SGPRs (the DMA below takes its LDS address and its
+// base as scalar operands).
+__device__ __forceinline__ uint32_t sgpr_u32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t sgpr_ptr(const void* p) {
+  const uint64_t b = (uint64_t)(uintptr_t)p;
+  return ((uint64_t)sgpr_u32((uint32_t)(b >> 32)) << 32) | sgpr_u32((uint32_t)b);
+}
+
 // 16 bytes per lane global → LDS: lane l's 16 bytes at sbase + voff land at
-// LDS byte address lds_byte + 16·l. M0 is written in the same statement;
-// nothing else in this file reads M0. Both the LDS address and the base must
-// be wave-uniform: they go through readfirstlane into SGPRs. A VMEM
-// instruction may read an SGPR only 5 wait states after a VALU instruction
-// (the readfirstlane) wrote it; the compiler cannot see the load inside the
-// asm string, so the statement supplies them itself (s_mov + s_nop 4), which
-// also covers the one wait state between the M0 write and its use.
+// LDS byte address lds_byte + 16·l. M0 is written in the same statement (one
+// wait state before its use); nothing else in this file reads M0. Callers
+// pass SGPR values made once per batch with sgpr_u32 / sgpr_ptr (and SALU
+// offsets from them). A VMEM instruction may read an SGPR only 5 wait states
+// after a VALU instruction (readfirstlane) wrote it, and the compiler, which
+// places the readfirstlane, cannot see the load inside the asm string: the
+// first DMA of a batch (PAD) supplies them itself with s_nop 4, the rest of
+// the batch reads SGPRs written long before. The build checks the generated
+// code for that (check_dma_hazard.py).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16_lds(uint32_t lds_byte, uint32_t voff, const void* sbase) {
-  const uint64_t b = (uint64_t)(uintptr_t)sbase;
-  const uint64_t ub = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
-                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-  const uint32_t ul = __builtin_amdgcn_readfirstlane(lds_byte);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(ul), "v"(voff),
-               "s"((const void*)(uintptr_t)ub)
-               : "memory", "m0");
+template <bool PAD = false>
+__device__ __forceinline__ void dma16_lds(uint32_t lds_byte, uint32_t voff, uint64_t sbase) {
+  if constexpr (PAD)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(lds_byte), "v"(voff),
+                 "s"((const void*)(uintptr_t)sbase)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:0" ::"s"(lds_byte), "v"(voff),
+                 "s"((const void*)(uintptr_t)sbase)
+                 : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -363,24 +375,31 @@ __global__ __launch_bounds__(320) void delta_chunk_scan_kernel(float* __restrict
   // wave 4: chunk c's W, K̃ᵀ and U slice into buffer bf by DMA
   auto dma_chunk = [&](uint32_t c, int bf) {
     const float* in = slot(c);
-    const uint32_t wl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Wb[bf];
-    const uint32_t kl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Kb[bf];
-    const uint32_t ul = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Ub[bf];
-#pragma unroll 4
-    for (int n = 0; n < 32; ++n) {  // W: LDS chunk 64 n + lane = row 2 n + lane / 32, slot lane % 32
+    const uint64_t bw = sgpr_ptr(in + kOffW), bk = sgpr_ptr(in + kOffKt), bu = sgpr_ptr(in + kOffU);
+    const uint32_t wl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Wb[bf]);
+    const uint32_t kl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Kb[bf]);
+    const uint32_t ul = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Ub[bf]);
+    // W: LDS chunk 64 n + lane = row 2 n + lane / 32, slot lane % 32
+    auto dma_w = [&](int n) {
       const int row = 2 * n + (lane >> 5), c4 = (lane & 31) ^ (row & 15);
-      dma16_lds(wl + n * 1024, (uint32_t)((row * DK + 4 * c4) * 4), in + kOffW);
-    }
+      return (uint32_t)((row * DK + 4 * c4) * 4);
+    };
+    dma16_lds<true>(wl, dma_w(0), bw);
 #pragma unroll 4
-    for (int n = 0; n < 32; ++n) {  // K̃ᵀ: row 4 n + lane / 16, slot lane % 16
+    for (int n = 1; n < 32; ++n) dma16_lds(wl + n * 1024, dma_w(n), bw);
+    // K̃ᵀ: row 4 n + lane / 16, slot lane % 16
+    auto dma_k = [&](int n) {
       const int row = 4 * n + (lane >> 4), c4 = (lane & 15) ^ (row & 15);
-      dma16_lds(kl + n * 1024, (uint32_t)((row * C + 4 * c4) * 4), in + kOffKt);
-    }
+      return (uint32_t)((row * C + 4 * c4) * 4);
+    };
+    dma16_lds<true>(kl, dma_k(0), bk);
+#pragma unroll 4
+    for (int n = 1; n < 32; ++n) dma16_lds(kl + n * 1024, dma_k(n), bk);
+    // U rows, columns dv0 .. + 16: row 16 n + lane / 4, chunk lane % 4
+    auto dma_u = [&](int n) { return (uint32_t)(((16 * n + (lane >> 2)) * DK + dv0 + 4 * (lane & 3)) * 4); };
+    dma16_lds<true>(ul, dma_u(0), bu);
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {  // U rows, columns dv0 .. + 16: row 16 n + lane / 4, chunk lane % 4
-      const int row = 16 * n + (lane >> 2);
-      dma16_lds(ul + n * 1024, (uint32_t)((row * DK + dv0 + 4 * (lane & 3)) * 4), in + kOffU);
-    }
+    for (int n = 1; n < 4; ++n) dma16_lds(ul + n * 1024, dma_u(n), bu);
   };
 
   if (wave == 4) {

@@ -36,11 +36,13 @@ struct TileArgs {
 
 // Geometry of one compiled tile variant.
 struct VariantInfo {
-  int fm;  // 16-row fragments per wave (and per workgroup: waves split N only)
+  int fm;  // 16-row fragments per wave
   int fn;  // 16-column fragments per wave
-  int wn;  // waves per workgroup
-  int bm() const { return 16 * fm; }
+  int wn;  // waves along N
+  int wm;  // waves along M
+  int bm() const { return 16 * fm * wm; }
   int bn() const { return 16 * fn * wn; }
+  int waves() const { return wm * wn; }
 };
 
 // The small-M weight-streaming kernel (gemm_stream.hip) over the members of

@@ -54,6 +54,9 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, f4 c) {
 }
 
 __device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
+// silu(g) · u in fp32, evaluated as the tile kernels evaluate it.
+__device__ __forceinline__ float swiglu_f(float g, float u) { return silu_f(g) * u; }
 }  // namespace
 
 __global__ __launch_bounds__(256) void gemm_stream_kernel(const TileArgs a) {
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(const TileArgs a) {
     const uint32_t m = 4 * g + e;
     if (m >= M) break;
     if (epi == 3u) {  // SwiGLU: columns n0 .. + 16 are the gate block, n0 + 16 .. + 16 the up block
-      if (ca < N) ((_Float16*)mb.y)[(size_t)m * ldy + n0 / 2 + r] = (_Float16)(silu_f(s0[e]) * s1[e]);
+      if (ca < N) ((_Float16*)mb.y)[(size_t)m * ldy + n0 / 2 + r] = (_Float16)swiglu_f(s0[e], s1[e]);
     } else if (epi == 1u) {
       _Float16* y = (_Float16*)mb.y + (size_t)m * ldy;
       if (ca < N) y[ca] = (_Float16)s0[e];

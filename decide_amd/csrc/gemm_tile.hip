@@ -7,7 +7,10 @@
 //
 //   * Workgroup = 4 wavefronts side by side along N, 64 columns each, every
 //     wave computing all BM = 16·FM rows of the tile with
-//     v_mfma_f32_16x16x32_f16 (BN = 256).
+//     v_mfma_f32_16x16x32_f16 (BN = 256). One more variant arranges the
+//     4 waves 2 x 2 with 5 x 9 fragments each (160 x 288): at M ≈ 603 the
+//     gate|up projection then makes exactly one tile per CU, and each wave
+//     reads fewer LDS rows per MFMA (80 + 144 instead of 208 + 64).
 //   * Both operands reach LDS by coalesced DMA (global_load_lds_dwordx4:
 //     eight lanes per 128-byte row segment, no VGPR staging). The MFMA B
 //     operand wants 16 different W rows per load instruction; gathered
@@ -61,6 +64,10 @@ __device__ __forceinline__ void static_for(Fn&& fn) {
 // each); decide's kernels use fast-math exp for silu as well (common.h:5-7).
 __device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
+// SwiGLU value silu(g) · u in fp32 (one helper for every epilogue, so all
+// kernels and tilings evaluate it with the same instructions).
+__device__ __forceinline__ float swiglu_f(float g, float u) { return silu_f(g) * u; }
+
 // Workgroup b runs on XCD b % 8. Renumber so XCD x owns one contiguous range
 // of work ids (a bijection on [0, G)).
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t G) {
@@ -69,15 +76,18 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t G) {
   return xcd * per + (xcd < rem ? xcd : rem) + local;
 }
 
-// Epilogue through LDS for the 4-wave, 256-column tiles: the accumulators of
-// CR = 64 rows at a time are written to LDS in row-major fp32 (row stride
-// BN + 4 floats: the four lane groups of a store land 16 banks apart), then
-// read back so that each wave writes whole output rows with 16-byte stores.
-// `stage` must hold 64 · 260 floats and be free (all main-loop LDS reads done).
-template <int FM, int FN>
+// Epilogue through LDS for the 4-wave tiles (WM waves along M, 4 / WM along
+// N, each wave FM x FN fragments): the accumulators of CR = 64 rows at a time
+// are written to LDS in row-major fp32 (row stride BN + 4 floats: the four
+// lane groups of a store land 16 banks apart), then read back so that each
+// wave writes whole output rows with 16-byte stores. `stage` must hold
+// 64 · (BN + 4) floats and be free (all main-loop LDS reads done).
+template <int FM, int FN, int WM>
 __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split,
                                                uint32_t m0, uint32_t n0, int wave, int r, int g, float* stage) {
-  constexpr int BN = 16 * FN * 4, LDR = BN + 4, CR = 64, BM = 16 * FM;
+  constexpr int WN = 4 / WM, BN = 16 * FN * WN, LDR = BN + 4, CR = 64, BM = 16 * FM * WM;
+  static_assert(WM == 1 || FN % 2 == 1, "2 x 2 layouts: SwiGLU handles one straddling pair (odd fragments per wave)");
+  const int rbase = (wave / WN) * 16 * FM, cbase = (wave % WN) * 16 * FN;  // this wave's sub-tile
   const uint32_t M = p.m, N = p.mem[mi].n;
   const int tid = threadIdx.x;
   const uint32_t epi = p.mem[mi].epi, ldy = p.mem[mi].ldy;
@@ -85,9 +95,11 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
   const bool partial = p.splits > 1;
   const uint32_t esz = (partial || epi == 0u || epi == 2u) ? 4u : 2u;
   const bool vec16 = partial || ((((uintptr_t)Y) % 16) == 0 && ((size_t)ldy * esz) % 16 == 0);
+  if constexpr (WM == 1) {
   if (epi == 3u && !partial) {
-    // SwiGLU in registers, then the fp16 tile [BM][BN/2] through LDS (row
-    // stride BN + 16 bytes) and out with 16-byte stores, 16 lanes per row.
+    // SwiGLU in registers (a wave holds whole gate|up pairs), then the fp16
+    // tile [BM][BN/2] through LDS (row stride BN + 16 bytes) and out with
+    // 16-byte stores, 16 lanes per row.
     constexpr int OW = BN / 2;          // output halves per tile row
     constexpr int LDH = OW + 8;         // LDS row stride in halves
     _Float16* st = (_Float16*)stage;
@@ -99,7 +111,7 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           st[(i * 16 + 4 * g + e) * LDH + wave * 8 * FN + (j / 2) * 16 + r] =
-              (_Float16)(silu_f(acc[i][j][e]) * acc[i][j + 1][e]);
+              (_Float16)swiglu_f(acc[i][j][e], acc[i][j + 1][e]);
     __syncthreads();
     constexpr int OQ = OW / 8;  // 16-byte chunks per row
 #pragma unroll
@@ -121,21 +133,88 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
     }
     return;
   }
+  } else if constexpr (FN % 2 == 1) {
+  if (epi == 3u && !partial) {
+    // 2 x 2 waves with an odd fragment count per wave: each wave holds 4 of
+    // its gate|up pairs whole (SwiGLU in registers, as above) and one half of
+    // the pair that straddles the two N halves, which goes through LDS in
+    // fp32 (gate from the left waves, up from the right ones).
+    constexpr int OW = BN / 2, LDH = OW + 8, PS = (FN - 1) / 2;  // PS: the straddling pair
+    _Float16* st = (_Float16*)stage;
+    float* gsp = (float*)(st + BM * LDH);  // [BM][16] gate, then [BM][16] up
+    float* usp = gsp + BM * 16;
+    __syncthreads();
+    // WNC: this wave's N half (compile time, so every accumulator index is a constant)
+    auto pairs = [&](auto wnc) {
+      constexpr int WNC = decltype(wnc)::value, J0 = WNC;  // local fragment J0 starts the first whole pair
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        static_for<0, (FN - J0) / 2>([&](auto qc) {
+          constexpr int j = J0 + 2 * decltype(qc)::value;  // local pair (j, j + 1)
+          constexpr int col = ((WNC * FN + j) / 2) * 16;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            st[(rbase + i * 16 + 4 * g + e) * LDH + col + r] = (_Float16)swiglu_f(acc[i][j][e], acc[i][j + 1][e]);
+        });
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (WNC == 0)
+            gsp[(rbase + i * 16 + 4 * g + e) * 16 + r] = acc[i][FN - 1][e];
+          else
+            usp[(rbase + i * 16 + 4 * g + e) * 16 + r] = acc[i][0][e];
+        }
+      }
+    };
+    if (wave % WN == 0)
+      pairs(std::integral_constant<int, 0>{});
+    else
+      pairs(std::integral_constant<int, 1>{});
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < (BM * 16 + 255) / 256; ++it) {
+      const int item = it * 256 + tid;
+      if (item >= BM * 16) break;
+      st[(item / 16) * LDH + PS * 16 + item % 16] = (_Float16)swiglu_f(gsp[item], usp[item]);
+    }
+    __syncthreads();
+    constexpr int OQ = OW / 8;  // 16-byte chunks per row
+#pragma unroll
+    for (int it = 0; it < (BM * OQ + 255) / 256; ++it) {
+      const int item = it * 256 + tid;
+      if (item >= BM * OQ) break;
+      const int row = item / OQ, oq = item % OQ;
+      const uint32_t grow = m0 + row;
+      if (grow >= M || n0 + 32 * (oq / 2) >= N) continue;
+      const h8 o = *(const h8*)(st + row * LDH + oq * 8);
+      _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + oq * 8;
+      if (vec16) {
+        __builtin_nontemporal_store(o, (h8*)dst);
+      } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int q = 0; q < 8; q += 2) *(h2*)(dst + q) = h2{o[q], o[q + 1]};
+      }
+    }
+    return;
+  }
+  }
   static_for<0, (BM + CR - 1) / CR>([&](auto cc) {
     constexpr int c0 = decltype(cc)::value * CR;
-    constexpr int i0 = c0 / 16, i1 = (c0 + CR) / 16 < FM ? (c0 + CR) / 16 : FM;
     constexpr int rows = (BM - c0) < CR ? (BM - c0) : CR;
     if (m0 + c0 >= M) return;
     __syncthreads();
 #pragma unroll
-    for (int i = i0; i < i1; ++i)
+    for (int i = 0; i < FM; ++i) {
+      const int tr = rbase + 16 * i;  // fragments never straddle a CR boundary
+      if (tr < c0 || tr >= c0 + CR) continue;
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          stage[(i * 16 - c0 + 4 * g + e) * LDR + wave * 16 * FN + j * 16 + r] = acc[i][j][e];
+        for (int e = 0; e < 4; ++e) stage[(tr - c0 + 4 * g + e) * LDR + cbase + j * 16 + r] = acc[i][j][e];
+    }
     __syncthreads();
-    // one float4 of a tile row per item; a wave covers one whole 256-column row
+    // SwiGLU reaches this path only as split-K partials (raw fp32; the reduce applies it).
+    // One float4 of a tile row per item.
 #pragma unroll
     for (int it = 0; it < (rows * (BN / 4) + 255) / 256; ++it) {
       const int item = it * 256 + tid;
@@ -217,26 +296,29 @@ __device__ __forceinline__ void dma16(uint32_t m0, uint32_t voff, const void* sb
 // X(kt + NBX - 1) and W(kt + NBW - 1). The DMAs a stage issues are ordered so
 // that the ones needed by the next stage come first; one vmcnt wait then
 // covers exactly those.
-template <int FM, int NBX, int NBW>
+template <int FM, int FN_, int WM, int NBX, int NBW>
 struct Pipe {
-  static constexpr int FN = 4, NT = 256, LAX = NBX - 1, LAW = NBW - 1;
+  static constexpr int FN = FN_, WN = 4 / WM, NT = 256, LAX = NBX - 1, LAW = NBW - 1;
   static constexpr int U = (NBX == NBW) ? NBX : NBX * NBW;  // unroll (lcm for 2, 3)
   static constexpr int LAM = LAX > LAW ? LAX : LAW;
-  static constexpr int BM = 16 * FM;
+  static constexpr int BM = 16 * FM * WM, BN = 16 * FN * WN;
   static constexpr int XR = (BM + 31) / 32 * 32;
   static constexpr int XPW = XR / 32;
-  static constexpr int WPW = 16 * FN / 8;
-  static constexpr int XBYTES = XR * 128, WBYTES = 256 * 128;
+  static constexpr int WPW = BN / 32;  // W DMAs per wave per stage (8 rows each)
+  static constexpr int XBYTES = XR * 128, WBYTES = BN * 128;
   static constexpr int WRING = NBX * XBYTES;  // offset of the W ring
   static constexpr int LDS_BYTES = NBX * XBYTES + NBW * WBYTES;
   // outstanding DMAs allowed at the end of a stage (those not needed next)
   static constexpr int KEEP = (LAX >= 2 ? XPW : 0) + (LAW >= 2 ? WPW : 0);
   static_assert(NBX >= 2 && NBW >= 2 && NBX <= 3 && NBW <= 3, "ring depths 2 or 3");
+  static_assert((WM == 1 && FN == 4) || WM == 2, "wave layouts: 1 x 4 with 4 fragments per wave, or 2 x 2");
+  static_assert(BN % 32 == 0, "whole 8-row DMA groups per wave");
 
   f4 acc[FM][FN];
   uint32_t xoff[XPW];
   uint32_t woff[WPW];
   uint32_t a0, a1;
+  uint32_t xrow;  // LDS byte offset of this wave's first X row (its M half)
   uint32_t lds_addr;
   uint32_t xm0[XPW];
   uint32_t wm0;
@@ -292,7 +374,7 @@ struct Pipe {
     constexpr int NF = 2 * FM, AD = 2, DPW = XPW + WPW;
     constexpr int NXS = (BX + LAX) % NBX, NWS = (BW + LAW) % NBW;
     const uint32_t xb = lds_addr + BX * XBYTES;
-    const uint32_t b0 = xb + a0, b1 = xb + a1;
+    const uint32_t b0 = xb + xrow + a0, b1 = xb + xrow + a1;
     const uint32_t wb = lds_addr + WRING + BW * WBYTES + wrow;
     const uint32_t w0 = wb + a0, w1 = wb + a1;
     h8 wf[FN][2];
@@ -366,11 +448,11 @@ struct Pipe {
   }
 };
 
-template <int FM, int NBX, int NBW>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
-void gemm_tile_kernel(const TileArgs p) {
-  using P = Pipe<FM, NBX, NBW>;
-  constexpr int FN = P::FN, BN = 16 * FN * 4;
+// One tile: FM x FN fragments per wave, WM waves along M and 4 / WM along N.
+template <int FM, int FN, int WM, int NBX, int NBW>
+__device__ __forceinline__ void tile_body(const TileArgs& p) {
+  using P = Pipe<FM, FN, WM, NBX, NBW>;
+  constexpr int BN = P::BN;
   constexpr int LDSB = P::LDS_BYTES > 64 * (BN + 4) * 4 ? P::LDS_BYTES : 64 * (BN + 4) * 4;
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
 
@@ -411,13 +493,14 @@ void gemm_tile_kernel(const TileArgs p) {
   }
 #pragma unroll
   for (int c = 0; c < P::WPW; ++c) {
-    const int G = 8 * wave + c;
+    const int G = P::WPW * wave + c;
     const uint32_t row = 8 * G + (lane >> 3);
     const uint32_t chunk = (uint32_t)((lane & 7) ^ ((4 * G + (lane >> 4)) & 7));
     pp.woff[c] = (min(n0 + row, N - 1) * ldw + chunk * 8) * 2;
   }
-  pp.wm0 = (uint32_t)wave * 8 * 1024;
-  pp.wrow = (uint32_t)wave * 64 * 128;
+  pp.wm0 = (uint32_t)(wave * P::WPW) * 1024;
+  pp.wrow = (uint32_t)((wave % P::WN) * 16 * FN) * 128;
+  pp.xrow = (uint32_t)((wave / P::WN) * 16 * FM) * 128;
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -472,13 +555,13 @@ void gemm_tile_kernel(const TileArgs p) {
     }
 #pragma unroll
     for (int c = 0; c < P::WPW; ++c) {
-      const int G = 8 * wave + c;
+      const int G = P::WPW * wave + c;
       const uint32_t chunk = (uint32_t)((lane & 7) ^ ((4 * G + (lane >> 4)) & 7));
       if (chunk < 4) dma16(pp.lds_addr + P::WRING + pp.wm0 + c * 1024, pp.woff[c], wb);
     }
     wait_vm<0>();
     __syncthreads();
-    const uint32_t b0 = pp.lds_addr + pp.a0;
+    const uint32_t b0 = pp.lds_addr + pp.xrow + pp.a0;
     const uint32_t w0 = pp.lds_addr + P::WRING + pp.wrow + pp.a0;
     h8 wf[FN];
     static_for<0, FN>([&](auto jc) {
@@ -500,7 +583,21 @@ void gemm_tile_kernel(const TileArgs p) {
     });
   }
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  store_tile_lds<FM, FN>(pp.acc, p, mi, split, m0, n0, wave, r, g, (float*)lds);
+  store_tile_lds<FM, FN, WM>(pp.acc, p, mi, split, m0, n0, wave, r, g, (float*)lds);
+}
+
+template <int FM, int NBX, int NBW>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_tile_kernel(const TileArgs p) {
+  tile_body<FM, 4, 1, NBX, NBW>(p);
+}
+
+// 2 x 2 waves, each FM x FN fragments: BM = 32·FM, BN = 32·FN. A gate|up
+// pair may straddle the two N halves, so SwiGLU runs from the staged tile.
+template <int FM, int FN, int NBX, int NBW>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_tile22_kernel(const TileArgs p) {
+  tile_body<FM, FN, 2, NBX, NBW>(p);
 }
 
 // ---- the compiled menu: (FM, NBX, NBW). BM = 16·FM rows, BN = 256.
@@ -524,8 +621,12 @@ struct VariantEntry {
   void (*fn)(const TileArgs);
 };
 
-#define DH_TILE_ENTRY(FM, NBX, NBW) {{FM, 4, 4}, gemm_tile_kernel<FM, NBX, NBW>},
-static const VariantEntry kVariants[] = {DH_TILE_MENU(DH_TILE_ENTRY)};
+#define DH_TILE_ENTRY(FM, NBX, NBW) {{FM, 4, 4, 1}, gemm_tile_kernel<FM, NBX, NBW>},
+static const VariantEntry kVariants[] = {
+    DH_TILE_MENU(DH_TILE_ENTRY)
+    // 160 x 288: at M ≈ 603 the gate|up projection is 4 x 64 = 256 tiles, one per CU
+    {{5, 9, 2, 2}, gemm_tile22_kernel<5, 9, 2, 3>},
+};
 #undef DH_TILE_ENTRY
 
 static_assert(sizeof(kVariants) / sizeof(kVariants[0]) <= 16, "the C ABI numbers other kernels from 16 on");
@@ -534,7 +635,7 @@ VariantInfo variant_info(int v) { return kVariants[v].info; }
 
 hipError_t launch_tile(int v, const TileArgs& a, uint32_t grid, hipStream_t s) {
   const VariantEntry& e = kVariants[v];
-  hipLaunchKernelGGL(e.fn, dim3(grid), dim3(64 * e.info.wn), 0, s, a);
+  hipLaunchKernelGGL(e.fn, dim3(grid), dim3(64 * e.info.wn * e.info.wm), 0, s, a);
   return hipGetLastError();
 }
 
@@ -558,7 +659,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, uint32_t spli
         us += *(const f4*)(pg + s * plane + kSwigluBlock);
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = silu_f(gs[q]) * us[q];
+      for (int q = 0; q < 4; ++q) v[q] = swiglu_f(gs[q], us[q]);
     } else {
       const float* pp = ws + (size_t)row * n + oc;
       v = *(const f4*)pp;
@@ -613,7 +714,7 @@ __global__ void gemm_reference_kernel(const _Float16* __restrict__ x, uint32_t l
   const size_t o = (size_t)row * ldy + oc;
   if (epi == 3u) {
     const uint32_t gc = (oc / kSwigluBlock) * 2 * kSwigluBlock + oc % kSwigluBlock;
-    ((_Float16*)y)[o] = (_Float16)(silu_f(dot(gc)) * dot(gc + kSwigluBlock));
+    ((_Float16*)y)[o] = (_Float16)swiglu_f(dot(gc), dot(gc + kSwigluBlock));
   } else {
     const float v = dot(oc);
     if (epi == 0u)

@@ -40,126 +40,127 @@ struct Measured {
 
 // {k, n, m, variant, splits}: fastest on an MI355X (gfx950, 256 CUs), the
 // variant index into the compiled menu (gemm_tile.hip: FM 1, 2, 4, 6, 8, 10,
-// 12, 13, 14, 5, 7, 9, 11), weights rotated over > 256 MB. Regenerate with
+// 12, 13, 14, 5, 7, 9, 11, then the 2 x 2 tile 160 x 288), weights rotated
+// over > 256 MB. Regenerate with
 // `python -m decide_amd.tune_gemm` after any change to the tile kernel.
 const Measured kMeasured[] = {
-    {2560, 12352, 1, 0, 4},  // 16.4 us
-    {2560, 12352, 3, 0, 4},  // 16.51 us
-    {2560, 12352, 8, 0, 4},  // 16.79 us
-    {2560, 12352, 16, 0, 4},  // 17.36 us
-    {2560, 12352, 24, 1, 4},  // 18.01 us
-    {2560, 12352, 48, 9, 4},  // 20.61 us
-    {2560, 12352, 96, 3, 4},  // 24.68 us
-    {2560, 12352, 163, 10, 2},  // 30.66 us
-    {2560, 12352, 276, 2, 1},  // 35.77 us
-    {2560, 12352, 490, 10, 1},  // 43.1 us
-    {2560, 12352, 603, 4, 1},  // 47.08 us
-    {2560, 12352, 1024, 7, 1},  // 65.71 us
-    {2560, 12352, 2307, 5, 1},  // 154.19 us
-    {2560, 10240, 1, 0, 6},  // 15.48 us
-    {2560, 10240, 3, 0, 4},  // 15.29 us
-    {2560, 10240, 8, 0, 4},  // 15.63 us
-    {2560, 10240, 16, 0, 4},  // 16.11 us
-    {2560, 10240, 24, 1, 6},  // 17.06 us
-    {2560, 10240, 48, 2, 6},  // 19.18 us
-    {2560, 10240, 96, 2, 3},  // 22.75 us
-    {2560, 10240, 163, 2, 2},  // 26.37 us
-    {2560, 10240, 276, 3, 2},  // 31.64 us
-    {2560, 10240, 490, 3, 1},  // 38.49 us
-    {2560, 10240, 603, 10, 1},  // 42.31 us
-    {2560, 10240, 1024, 12, 1},  // 57.17 us
-    {2560, 10240, 2307, 7, 1},  // 126.24 us
-    {2560, 18432, 1, 0, 3},  // 21.74 us
-    {2560, 18432, 3, 0, 3},  // 22.06 us
-    {2560, 18432, 8, 0, 3},  // 22.53 us
-    {2560, 18432, 16, 0, 3},  // 22.7 us
-    {2560, 18432, 24, 1, 3},  // 23.62 us
-    {2560, 18432, 48, 3, 3},  // 26.68 us
-    {2560, 18432, 96, 6, 3},  // 32.52 us
-    {2560, 18432, 163, 2, 1},  // 35.81 us
-    {2560, 18432, 276, 4, 1},  // 39.67 us
-    {2560, 18432, 490, 12, 1},  // 49.11 us
-    {2560, 18432, 603, 7, 1},  // 54.32 us
-    {2560, 18432, 1024, 5, 1},  // 87.51 us
-    {2560, 18432, 2307, 12, 1},  // 200.13 us
-    {4096, 2560, 1, 0, 8},  // 11.35 us
-    {4096, 2560, 3, 0, 6},  // 11.68 us
-    {4096, 2560, 8, 0, 6},  // 11.8 us
-    {4096, 2560, 16, 0, 6},  // 12.18 us
-    {4096, 2560, 24, 0, 6},  // 12.26 us
-    {4096, 2560, 48, 0, 6},  // 12.91 us
-    {4096, 2560, 96, 1, 6},  // 14.01 us
-    {4096, 2560, 163, 1, 4},  // 17.4 us
-    {4096, 2560, 276, 9, 6},  // 19.82 us
-    {4096, 2560, 490, 3, 4},  // 24.3 us
-    {4096, 2560, 603, 10, 4},  // 27.29 us
-    {4096, 2560, 1024, 4, 3},  // 36.55 us
-    {4096, 2560, 2307, 3, 1},  // 57.9 us
-    {9216, 2560, 1, 0, 8},  // 19.51 us
-    {9216, 2560, 3, 0, 8},  // 19.42 us
-    {9216, 2560, 8, 0, 8},  // 19.87 us
-    {9216, 2560, 16, 0, 8},  // 20.5 us
-    {9216, 2560, 24, 0, 8},  // 20.34 us
-    {9216, 2560, 48, 0, 8},  // 20.89 us
-    {9216, 2560, 96, 1, 8},  // 22.66 us
-    {9216, 2560, 163, 2, 8},  // 25.33 us
-    {9216, 2560, 276, 3, 8},  // 29.07 us
-    {9216, 2560, 490, 4, 6},  // 37.63 us
-    {9216, 2560, 603, 10, 4},  // 42.71 us
-    {9216, 2560, 1024, 4, 3},  // 58.78 us
-    {9216, 2560, 2307, 3, 1},  // 114.9 us
-    {2560, 2048, 1, 1, 6},  // 10.28 us
-    {2560, 2048, 3, 0, 6},  // 10.0 us
-    {2560, 2048, 8, 0, 4},  // 10.32 us
-    {2560, 2048, 16, 0, 6},  // 10.75 us
-    {2560, 2048, 24, 0, 4},  // 10.74 us
-    {2560, 2048, 48, 0, 4},  // 10.97 us
-    {2560, 2048, 96, 0, 4},  // 12.08 us
-    {2560, 2048, 163, 1, 4},  // 13.58 us
-    {2560, 2048, 276, 1, 3},  // 14.83 us
-    {2560, 2048, 490, 1, 2},  // 16.95 us
-    {2560, 2048, 603, 2, 3},  // 18.1 us
-    {2560, 2048, 1024, 2, 2},  // 22.32 us
-    {2560, 2048, 2307, 3, 1},  // 32.39 us
-    {2560, 8192, 1, 0, 4},  // 14.22 us
-    {2560, 8192, 3, 0, 6},  // 14.16 us
-    {2560, 8192, 8, 0, 6},  // 14.35 us
-    {2560, 8192, 16, 0, 4},  // 15.0 us
-    {2560, 8192, 24, 0, 4},  // 15.05 us
-    {2560, 8192, 48, 1, 4},  // 16.34 us
-    {2560, 8192, 96, 2, 4},  // 19.55 us
-    {2560, 8192, 163, 3, 4},  // 22.59 us
-    {2560, 8192, 276, 9, 2},  // 28.11 us
-    {2560, 8192, 490, 2, 1},  // 35.49 us
-    {2560, 8192, 603, 9, 1},  // 38.71 us
-    {2560, 8192, 1024, 4, 1},  // 47.05 us
-    {2560, 8192, 2307, 5, 1},  // 101.74 us
-    {2560, 6144, 1, 0, 6},  // 13.22 us
-    {2560, 6144, 3, 0, 6},  // 13.3 us
-    {2560, 6144, 8, 0, 6},  // 13.56 us
-    {2560, 6144, 16, 0, 6},  // 14.14 us
-    {2560, 6144, 24, 0, 4},  // 14.36 us
-    {2560, 6144, 48, 1, 4},  // 15.79 us
-    {2560, 6144, 96, 2, 4},  // 18.17 us
-    {2560, 6144, 163, 2, 3},  // 20.95 us
-    {2560, 6144, 276, 2, 2},  // 24.72 us
-    {2560, 6144, 490, 10, 2},  // 31.56 us
-    {2560, 6144, 603, 2, 1},  // 34.3 us
-    {2560, 6144, 1024, 10, 1},  // 41.04 us
-    {2560, 6144, 2307, 4, 1},  // 87.03 us
-    {2560, 9216, 1, 0, 6},  // 14.48 us
-    {2560, 9216, 3, 0, 4},  // 14.49 us
-    {2560, 9216, 8, 0, 4},  // 14.82 us
-    {2560, 9216, 16, 0, 4},  // 15.4 us
-    {2560, 9216, 24, 1, 6},  // 16.16 us
-    {2560, 9216, 48, 2, 6},  // 18.46 us
-    {2560, 9216, 96, 2, 3},  // 21.3 us
-    {2560, 9216, 163, 2, 2},  // 25.14 us
-    {2560, 9216, 276, 3, 2},  // 30.45 us
-    {2560, 9216, 490, 9, 1},  // 37.48 us
-    {2560, 9216, 603, 3, 1},  // 39.89 us
-    {2560, 9216, 1024, 5, 1},  // 52.0 us
-    {2560, 9216, 2307, 12, 1},  // 111.62 us
+    {2560, 12352, 1, 0, 4},  // 16.37 us
+    {2560, 12352, 3, 0, 4},  // 16.98 us
+    {2560, 12352, 8, 0, 4},  // 16.83 us
+    {2560, 12352, 16, 0, 4},  // 17.39 us
+    {2560, 12352, 24, 1, 4},  // 18.04 us
+    {2560, 12352, 48, 2, 4},  // 20.25 us
+    {2560, 12352, 96, 3, 4},  // 24.65 us
+    {2560, 12352, 163, 10, 2},  // 31.3 us
+    {2560, 12352, 276, 2, 1},  // 35.73 us
+    {2560, 12352, 490, 10, 1},  // 44.69 us
+    {2560, 12352, 603, 4, 1},  // 47.89 us
+    {2560, 12352, 1024, 7, 1},  // 67.67 us
+    {2560, 12352, 2307, 5, 1},  // 157.29 us
+    {2560, 10240, 1, 0, 4},  // 15.07 us
+    {2560, 10240, 3, 1, 4},  // 15.65 us
+    {2560, 10240, 8, 0, 4},  // 15.68 us
+    {2560, 10240, 16, 0, 4},  // 16.13 us
+    {2560, 10240, 24, 1, 4},  // 17.01 us
+    {2560, 10240, 48, 2, 4},  // 18.98 us
+    {2560, 10240, 96, 1, 2},  // 22.51 us
+    {2560, 10240, 163, 2, 2},  // 26.28 us
+    {2560, 10240, 276, 3, 2},  // 32.29 us
+    {2560, 10240, 490, 3, 1},  // 39.38 us
+    {2560, 10240, 603, 10, 1},  // 43.38 us
+    {2560, 10240, 1024, 12, 1},  // 58.49 us
+    {2560, 10240, 2307, 7, 1},  // 131.46 us
+    {2560, 18432, 1, 0, 3},  // 21.61 us
+    {2560, 18432, 3, 0, 3},  // 21.74 us
+    {2560, 18432, 8, 0, 3},  // 22.06 us
+    {2560, 18432, 16, 0, 3},  // 22.64 us
+    {2560, 18432, 24, 1, 3},  // 23.59 us
+    {2560, 18432, 48, 9, 3},  // 26.43 us
+    {2560, 18432, 96, 12, 3},  // 32.55 us
+    {2560, 18432, 163, 2, 1},  // 35.71 us
+    {2560, 18432, 276, 3, 1},  // 40.14 us
+    {2560, 18432, 490, 12, 1},  // 50.69 us
+    {2560, 18432, 603, 13, 1},  // 54.81 us
+    {2560, 18432, 1024, 5, 1},  // 90.08 us
+    {2560, 18432, 2307, 12, 1},  // 201.23 us
+    {4096, 2560, 1, 0, 6},  // 11.41 us
+    {4096, 2560, 3, 0, 8},  // 11.82 us
+    {4096, 2560, 8, 0, 6},  // 12.32 us
+    {4096, 2560, 16, 1, 6},  // 12.84 us
+    {4096, 2560, 24, 0, 8},  // 12.88 us
+    {4096, 2560, 48, 0, 6},  // 13.87 us
+    {4096, 2560, 96, 1, 8},  // 15.44 us
+    {4096, 2560, 163, 2, 8},  // 17.23 us
+    {4096, 2560, 276, 9, 6},  // 20.03 us
+    {4096, 2560, 490, 3, 4},  // 25.49 us
+    {4096, 2560, 603, 10, 4},  // 27.83 us
+    {4096, 2560, 1024, 4, 3},  // 37.74 us
+    {4096, 2560, 2307, 3, 1},  // 58.95 us
+    {9216, 2560, 1, 0, 8},  // 19.39 us
+    {9216, 2560, 3, 0, 8},  // 19.55 us
+    {9216, 2560, 8, 0, 8},  // 19.95 us
+    {9216, 2560, 16, 0, 8},  // 20.44 us
+    {9216, 2560, 24, 0, 8},  // 20.78 us
+    {9216, 2560, 48, 0, 8},  // 20.87 us
+    {9216, 2560, 96, 1, 8},  // 22.4 us
+    {9216, 2560, 163, 2, 8},  // 25.43 us
+    {9216, 2560, 276, 3, 8},  // 30.02 us
+    {9216, 2560, 490, 4, 6},  // 38.09 us
+    {9216, 2560, 603, 10, 4},  // 43.48 us
+    {9216, 2560, 1024, 4, 3},  // 59.85 us
+    {9216, 2560, 2307, 3, 1},  // 116.32 us
+    {2560, 2048, 1, 0, 6},  // 10.06 us
+    {2560, 2048, 3, 0, 6},  // 10.23 us
+    {2560, 2048, 8, 0, 6},  // 10.61 us
+    {2560, 2048, 16, 0, 4},  // 10.8 us
+    {2560, 2048, 24, 0, 4},  // 10.99 us
+    {2560, 2048, 48, 0, 4},  // 11.27 us
+    {2560, 2048, 96, 0, 4},  // 11.67 us
+    {2560, 2048, 163, 1, 4},  // 13.15 us
+    {2560, 2048, 276, 2, 3},  // 15.83 us
+    {2560, 2048, 490, 2, 4},  // 16.72 us
+    {2560, 2048, 603, 2, 3},  // 17.93 us
+    {2560, 2048, 1024, 2, 2},  // 22.5 us
+    {2560, 2048, 2307, 3, 1},  // 33.38 us
+    {2560, 8192, 1, 0, 6},  // 13.97 us
+    {2560, 8192, 3, 0, 6},  // 14.18 us
+    {2560, 8192, 8, 0, 4},  // 14.62 us
+    {2560, 8192, 16, 0, 6},  // 15.0 us
+    {2560, 8192, 24, 0, 4},  // 15.22 us
+    {2560, 8192, 48, 1, 4},  // 16.33 us
+    {2560, 8192, 96, 2, 4},  // 18.92 us
+    {2560, 8192, 163, 3, 4},  // 24.05 us
+    {2560, 8192, 276, 9, 2},  // 28.71 us
+    {2560, 8192, 490, 2, 1},  // 35.73 us
+    {2560, 8192, 603, 3, 1},  // 39.32 us
+    {2560, 8192, 1024, 4, 1},  // 47.95 us
+    {2560, 8192, 2307, 5, 1},  // 104.01 us
+    {2560, 6144, 1, 0, 6},  // 13.03 us
+    {2560, 6144, 3, 0, 6},  // 13.27 us
+    {2560, 6144, 8, 0, 6},  // 13.73 us
+    {2560, 6144, 16, 0, 8},  // 14.19 us
+    {2560, 6144, 24, 0, 4},  // 14.53 us
+    {2560, 6144, 48, 1, 4},  // 15.63 us
+    {2560, 6144, 96, 2, 4},  // 17.86 us
+    {2560, 6144, 163, 2, 3},  // 21.06 us
+    {2560, 6144, 276, 2, 2},  // 24.82 us
+    {2560, 6144, 490, 10, 2},  // 32.39 us
+    {2560, 6144, 603, 2, 1},  // 34.7 us
+    {2560, 6144, 1024, 10, 1},  // 42.45 us
+    {2560, 6144, 2307, 4, 1},  // 88.02 us
+    {2560, 9216, 1, 0, 4},  // 14.49 us
+    {2560, 9216, 3, 0, 4},  // 14.66 us
+    {2560, 9216, 8, 0, 4},  // 15.05 us
+    {2560, 9216, 16, 0, 6},  // 15.51 us
+    {2560, 9216, 24, 0, 3},  // 17.05 us
+    {2560, 9216, 48, 2, 4},  // 18.27 us
+    {2560, 9216, 96, 2, 3},  // 21.76 us
+    {2560, 9216, 163, 2, 2},  // 25.15 us
+    {2560, 9216, 276, 3, 2},  // 30.91 us
+    {2560, 9216, 490, 9, 1},  // 38.08 us
+    {2560, 9216, 603, 3, 1},  // 39.9 us
+    {2560, 9216, 1024, 5, 1},  // 53.39 us
+    {2560, 9216, 2307, 12, 1},  // 116.93 us
 };
 }  // namespace
 
@@ -188,7 +189,8 @@ double plan_estimate_us(int variant, uint32_t splits, uint32_t m, uint32_t n, ui
   const double mtiles = ceil_div(m, (uint32_t)v.bm()), stripes = ceil_div(n, (uint32_t)v.bn());
   const double blocks = mtiles * stripes * splits;
   const double rounds = std::ceil(blocks / kCUs);
-  const double stage_us = std::max(kMinStageUs, kStageUsPerFM * v.fm);
+  // MFMAs per wave per stage, in units of a 16-row fragment of the 4-fragment-wide waves
+  const double stage_us = std::max(kMinStageUs, kStageUsPerFM * v.fm * v.fn / 4.0);
   const double compute_us = rounds * st_per_split * stage_us;
   const double out_b = (epi == 0u || epi == 2u) ? 4.0 : 2.0;
   const double out_cols = epi == 3u ? n / 2.0 : n;

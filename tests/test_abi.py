@@ -107,8 +107,9 @@ def test_variant_menu_geometry():
     vs = variants()
     assert len(vs) >= 8
     for v in vs:
-        assert v["bm"] % 16 == 0 and v["bn"] % 32 == 0
-        assert v["wave_cols"] % 32 == 0  # SwiGLU pairs 16-column fragments inside a wave
+        assert v["bm"] % 16 == 0 and v["bn"] % 32 == 0  # a tile holds whole gate|up pairs (2 x 16 columns)
+        assert v["wave_cols"] % 16 == 0 and v["waves"] == 4
+        assert v["bn"] % v["wave_cols"] == 0 and v["bm"] % 16 == 0
 
 
 @pytest.mark.parametrize("m", [1, 8, 16, 163, 276, 300, 493, 512, 603, 2307])

@@ -147,6 +147,29 @@ def test_every_variant_swiglu_and_add(gpu, kernels, stream, variant):
         kernels.gemm.force(None)
 
 
+def test_every_variant_stores_the_same_bits(gpu, kernels, stream):
+    """Every tile variant sums K in the same order (64-wide stages, two 32-wide MFMA steps, the same lane
+    split of k), so without split-K they store identical bits for every epilogue, whatever the tiling:
+    the 2 x 2 tile's SwiGLU pair that straddles its two N halves included (n covers 9 tiles of 256 and
+    8 of 288 columns, m several row tiles with a ragged last one)."""
+    m, n, k = 203, 2304, 320
+    x, w = inputs(m, n, k, 77)
+    y0 = synth.normal_f32(synth.seed_for(78), (m, n), 1.0)
+    try:
+        for epi in (Epilogue.SwigluF16, Epilogue.StoreF32, Epilogue.AddF32, Epilogue.StoreF16):
+            ref = None
+            for v in range(len(variants())):
+                kernels.gemm.force(v, 1)
+                got = run_gemm(kernels, stream, x, w, epi, y0 if epi == Epilogue.AddF32 else None)
+                if ref is None:
+                    ref = got
+                    check_gemm(f"variant 0 {epi.name}", got, oracle_epi(x, w, epi, y0))
+                else:
+                    assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), f"variant {v} {epi.name}"
+    finally:
+        kernels.gemm.force(None)
+
+
 def test_reference_kernel_matches_oracle(gpu, kernels_ref, stream):
     for (m, n, k) in [(5, 64, 96), (33, 96, 160), (70, 128, 2560)]:
         x, w = inputs(m, n, k, 400 + m)
