@@ -457,10 +457,13 @@ __device__ __forceinline__ void tile_body(const TileArgs& p) {
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
 
   const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
+  // Work order: M tiles fastest, then column stripes, then K splits, so the
+  // consecutive work ids one XCD runs share one K range of X (and each
+  // stripe's W block is read by its M tiles back to back).
   const uint32_t mt = wid % p.mtiles;
   const uint32_t q = wid / p.mtiles;
-  const uint32_t split = q % p.splits;
-  const uint32_t gs = q / p.splits;
+  const uint32_t gs = q % p.nstripes;
+  const uint32_t split = q / p.nstripes;
   int mi = 0;
 #pragma unroll
   for (int i = 1; i < kMaxMembers; ++i)

@@ -90,11 +90,11 @@ const Measured kMeasured[] = {
     {4096, 2560, 24, 0, 8},  // 12.88 us
     {4096, 2560, 48, 0, 6},  // 13.87 us
     {4096, 2560, 96, 1, 8},  // 15.44 us
-    {4096, 2560, 163, 2, 8},  // 17.23 us
-    {4096, 2560, 276, 9, 6},  // 20.03 us
-    {4096, 2560, 490, 3, 4},  // 25.49 us
-    {4096, 2560, 603, 10, 4},  // 27.83 us
-    {4096, 2560, 1024, 4, 3},  // 37.74 us
+    {4096, 2560, 163, 1, 4},  // 17.56 us
+    {4096, 2560, 276, 9, 6},  // 19.85 us
+    {4096, 2560, 490, 3, 4},  // 24.16 us
+    {4096, 2560, 603, 10, 4},  // 26.87 us
+    {4096, 2560, 1024, 4, 3},  // 36.27 us
     {4096, 2560, 2307, 3, 1},  // 58.95 us
     {9216, 2560, 1, 0, 8},  // 19.39 us
     {9216, 2560, 3, 0, 8},  // 19.55 us
@@ -103,11 +103,11 @@ const Measured kMeasured[] = {
     {9216, 2560, 24, 0, 8},  // 20.78 us
     {9216, 2560, 48, 0, 8},  // 20.87 us
     {9216, 2560, 96, 1, 8},  // 22.4 us
-    {9216, 2560, 163, 2, 8},  // 25.43 us
-    {9216, 2560, 276, 3, 8},  // 30.02 us
-    {9216, 2560, 490, 4, 6},  // 38.09 us
-    {9216, 2560, 603, 10, 4},  // 43.48 us
-    {9216, 2560, 1024, 4, 3},  // 59.85 us
+    {9216, 2560, 163, 2, 8},  // 24.71 us
+    {9216, 2560, 276, 3, 8},  // 28.55 us
+    {9216, 2560, 490, 4, 6},  // 36.6 us
+    {9216, 2560, 603, 5, 6},  // 41.7 us
+    {9216, 2560, 1024, 4, 3},  // 57.89 us
     {9216, 2560, 2307, 3, 1},  // 116.32 us
     {2560, 2048, 1, 0, 6},  // 10.06 us
     {2560, 2048, 3, 0, 6},  // 10.23 us
