@@ -17,7 +17,12 @@ decide reports its GEMMs the same way per shape in its planner notes
 (crates/decide-metal/src/gemm_configs.rs:247-309); the algorithmic byte/flop
 formulas follow its GEMM contract (kernels/gemm.rs:126-137).
 
-Usage: python -m decide_amd.shape_report [--iters 200] [--json out.json] [--md out.md]
+With --markers (for runs under rocprofv3 --pmc), one device-to-device copy of
+CALIBRATION_BYTES comes first (the reference for the FETCH_SIZE / WRITE_SIZE
+byte scale), and a 1 MB memset runs before each shape, so that
+decide_amd/pmc_report.py can cut the counter dispatch stream into shapes.
+
+Usage: python -m decide_amd.shape_report [--iters 200] [--json out.json] [--md out.md] [--markers]
 """
 
 from __future__ import annotations
@@ -41,6 +46,8 @@ PEAK_GBS = 8000.0
 RIDGE = PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9)
 POOL_BYTES = 640 << 20
 MIN_ROTATION_BYTES = 300 << 20
+CALIBRATION_BYTES = 94371840  # one device-to-device copy under --markers (the counter byte-scale reference)
+MARKER_BYTES = 1 << 20  # memset between shapes under --markers
 
 # (name, M, K, [(N, epi), ...]) — one entry = one launch (a grouped launch if several members)
 SHAPES = [
@@ -126,6 +133,7 @@ def main():
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--json", default="")
     ap.add_argument("--md", default="")
+    ap.add_argument("--markers", action="store_true", help="calibration copy + a memset before each shape")
     args = ap.parse_args()
     if not hip.available():
         sys.exit("no GPU")
@@ -142,9 +150,26 @@ def main():
     y.zero_()
     k.gemm.warm_up(s, maxm)
     st.synchronize()
+    marker_buf = None
+    if args.markers:
+        src = DeviceArray((CALIBRATION_BYTES // 2,), np.float16)
+        dst = DeviceArray((CALIBRATION_BYTES // 2,), np.float16)
+        src.zero_()
+        dst.copy_(src)
+        hip.synchronize()
+        src.free()
+        dst.free()
+        marker_buf = DeviceArray((MARKER_BYTES // 4,), np.float32)
+
+    def marker():
+        if marker_buf is not None:
+            marker_buf.zero_()
+            hip.synchronize()
+
     loaded = k.gemm.fast_pipelines()
     results = []
     for name, m, kk, members in SHAPES:
+        marker()
         wbytes = sum(n * kk * 2 for n, _ in members)
         copies = max(1, min(POOL_BYTES // wbytes, -(-MIN_ROTATION_BYTES // wbytes)))
         state = {"i": 0}
@@ -172,6 +197,7 @@ def main():
         results.append(dict(name=name, m=m, k=kk, n=[n for n, _ in members], epi=[e.name for _, e in members],
                             us_mean=mean_us, us_median=med_us, flops=fl, bytes=by, rotation=copies, plan=plan))
     assert k.gemm.fast_pipelines() == loaded, "a GEMM kernel was loaded after warm-up"
+    marker()
     us, fl, by = head_shape(k, st, args.iters)
     results.append(dict(name="C4 head 24x64 (bf16 gather)", m=24, k=2560, n=[64], epi=["head"], us_mean=us[0],
                         us_median=us[1], flops=fl, bytes=by, rotation=1, plan=None))
