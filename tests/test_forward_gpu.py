@@ -57,9 +57,10 @@ def _run(model, kernels, ids, ans, cand, ncand, max_cand, prune):
     return to_host(logits)
 
 
-@pytest.mark.parametrize("layers,t,prune", [(4, 48, True), (4, 40, False), (8, 70, True)])
+# (4, 330): past DH_DELTA_CHUNK_MIN_T, so the default context runs the chunked recurrence end to end
+@pytest.mark.parametrize("layers,t,prune", [(4, 48, True), (4, 40, False), (8, 70, True), (4, 330, True)])
 def test_forward_matches_oracle(gpu, kernels, layers, t, prune):
-    cfg = ModelConfig(layers=layers, vocab=1000, max_tokens=96, max_answers=4, max_cand=8)
+    cfg = ModelConfig(layers=layers, vocab=1000, max_tokens=max(96, t), max_answers=4, max_cand=8)
     model = Model(kernels.ctx, cfg)
     kernels.gemm.warm_up(0, max_m=cfg.max_tokens)
     model.init_random(0, seed=1234 + layers)
