@@ -132,6 +132,32 @@ def test_planner_covers_engine_shapes(m, kn):
         assert p["ws_bytes"] <= 512 << 20
 
 
+def test_planner_invariants_on_random_shapes():
+    """Any legal shape gets a plan whose grid covers the output once per split, with no empty split
+    (splits <= the 64-wide K stages, or the 128-wide ones of the weight-streaming kernel), a workspace
+    of exactly splits x M x N fp32 partials when split, and the workspace cap respected."""
+    rng = np.random.default_rng(7)
+    vs = variants()
+    for _ in range(400):
+        m = int(rng.choice([rng.integers(1, 17), rng.integers(17, 700), rng.integers(700, 4097)]))
+        n = 32 * int(rng.integers(1, 1025))
+        k = 32 * int(rng.integers(1, 513))
+        epi = Epilogue(int(rng.integers(0, 4)))
+        p = plan_for(m, n, k, epi)
+        name = f"m{m} n{n} k{k} {epi.name}: {p}"
+        if p["variant"] == _lib.DH_GEMM_STREAM_VARIANT:
+            assert m <= 16 and k % 128 == 0 and p["bm"] == 16 and p["bn"] == 32, name
+            assert p["splits"] <= k // 128, name
+        else:
+            v = vs[p["variant"]]
+            assert p["bm"] == v["bm"] and p["bn"] == v["bn"] and p["waves"] == v["waves"], name
+            assert p["splits"] <= -(-k // 64), name
+        assert p["splits"] >= 1, name
+        assert p["workgroups"] == -(-m // p["bm"]) * -(-n // p["bn"]) * p["splits"], name
+        assert p["ws_bytes"] == (p["splits"] * m * n * 4 if p["splits"] > 1 else 0), name
+        assert p["ws_bytes"] <= 512 << 20, name
+
+
 def test_layout_functions_match_oracle():
     import oracle_lib as orc
 

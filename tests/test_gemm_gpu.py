@@ -353,3 +353,62 @@ def test_config4_projections_m2307(gpu, kernels, stream, kn):
     else:
         want = y
     check_gemm(f"C4 k{k} n{n}", got[rows], want)
+
+
+def random_shapes(count: int, seed: int):
+    """Seeded shapes across the planner's range: M from 1 (the weight-streaming kernel) to ~1300, N and K
+    any multiple of 32 (so K % 64 == 32 leaves a half stage, split-K included), row strides padded past
+    K and the output width, every epilogue. M·N·K stays small enough for the oracle."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        r = rng.random()
+        m = int(rng.integers(1, 17)) if r < 0.2 else int(rng.integers(17, 420)) if r < 0.8 else int(rng.integers(420, 1300))
+        n = 32 * int(rng.integers(1, 72))
+        k = 32 * int(rng.integers(1, 90))
+        if m * n * k > 6e8:
+            continue
+        epi = Epilogue(int(rng.integers(0, 4)))
+        pads = [8 * int(rng.integers(0, 3)) for _ in range(3)]  # extra elements of ldx, ldw, ldy
+        forced = (int(rng.integers(0, len(variants()))), int(rng.integers(1, 5)))
+        out.append((m, n, k, epi, pads, forced))
+    return out
+
+
+@pytest.mark.parametrize("case", range(32))
+def test_random_shapes_planner_and_forced(gpu, kernels, stream, case):
+    """One seeded shape through the planner's own choice and through one forced (variant, split-K) pair:
+    both within the GEMM bar of the oracle, and nothing outside the output window written."""
+    m, n, k, epi, (px, pw, py), forced = random_shapes(32, 2024)[case]
+    ldx, ldw = k + px, k + pw
+    out_cols = n // 2 if epi == Epilogue.SwigluF16 else n
+    ldy = out_cols + py
+    dt = np.float32 if epi in (Epilogue.StoreF32, Epilogue.AddF32) else np.float16
+    x, w = inputs(m, n, k, 900 + case)
+    xbig = np.zeros((m, ldx), np.float16)
+    wbig = np.zeros((n, ldw), np.float16)
+    xbig[:, :k], wbig[:, :k] = x, w
+    xbig[:, k:], wbig[:, k:] = np.float16(np.inf), np.float16(np.inf)  # must never reach a sum
+    y0 = synth.normal_f32(synth.seed_for(950 + case), (m, ldy), 1.0).astype(dt)
+    if epi != Epilogue.AddF32:
+        y0[:] = 7.0
+    want = oracle_epi(x, w, epi, y0[:, :n].astype(np.float32) if epi == Epilogue.AddF32 else None)
+    xd, wd = to_dev(xbig), to_dev(wbig)
+    name = f"case {case}: m{m} n{n} k{k} {epi.name} ld {ldx}/{ldw}/{ldy}"
+    tol = 2e-3 if epi in (Epilogue.StoreF16, Epilogue.SwigluF16) else 1e-4
+    try:
+        for pin in (None, forced):
+            if pin is not None:
+                kernels.gemm.force(*pin)
+            plan = kernels.gemm.plan(m, n, k, epi)
+            label = f"{name} variant {plan['variant']} splits {plan['splits']}"
+            print(label, flush=True)
+            y = to_dev(y0)
+            kernels.gemm.gemm(stream, (xd, 0), (wd, 0), (y, 0), m, n, k, ldx, ldw, ldy, epi)
+            sync()
+            got = to_host(y)
+            check_gemm(label, got[:, :out_cols].astype(np.float32), want)
+            orc.assert_close(label, got[:, :out_cols].astype(np.float32), want, atol=tol, rtol=tol)
+            assert np.array_equal(got[:, out_cols:].view(np.uint8), y0[:, out_cols:].view(np.uint8)), label
+    finally:
+        kernels.gemm.force(None)
