@@ -231,8 +231,10 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
   if (!members || count < 1 || count > (uint32_t)dh::kMaxMembers)
     return fail(DH_EINVAL, "gemm grouped: count = %u must be in 1..%d", count, dh::kMaxMembers);
   uint32_t n_total = 0;
+  uint32_t ns[dh::kMaxMembers];
   for (uint32_t i = 0; i < count; ++i) {
     const dh_gemm_member& mb = members[i];
+    ns[i] = mb.n;
     int rc = check_gemm(x, ldx, mb.w, mb.ldw, mb.y, mb.ldy, m, mb.n, k, mb.epi);
     if (rc != DH_OK) {
       std::string msg = g_err;
@@ -254,7 +256,7 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
     return ok();
   }
   dh::Plan p = ctx->forced_variant >= 0 ? dh::plan_make(ctx->forced_variant, 1, m, n_total, k, 0u)
-                                        : dh::plan_grouped(m, n_total, k);
+                                        : dh::plan_grouped(m, k, ns, count);
   if (p.variant < 0) return fail(DH_EINVAL, "gemm grouped: no plan");
   return launch_plan(ctx, s, p, x, ldx, m, k, members, count);
 }

@@ -68,6 +68,12 @@ __device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_r
 // kernels and tilings evaluate it with the same instructions).
 __device__ __forceinline__ float swiglu_f(float g, float u) { return silu_f(g) * u; }
 
+// Keeps an accumulator fragment in AGPRs up to this point of the epilogue, so
+// that the fragments move to VGPRs one at a time as they are stored; left to
+// itself the compiler copies them all at the loop exit, which for the largest
+// tiles needs more VGPRs than there are.
+__device__ __forceinline__ void pin_acc(f4& v) { asm volatile("" : "+a"(v)); }
+
 // Workgroup b runs on XCD b % 8. Renumber so XCD x owns one contiguous range
 // of work ids (a bijection on [0, G)).
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t G) {
@@ -83,7 +89,7 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t G) {
 // wave writes whole output rows with 16-byte stores. `stage` must hold
 // 64 · (BN + 4) floats and be free (all main-loop LDS reads done).
 template <int FM, int FN, int WM>
-__device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split,
+__device__ __forceinline__ void store_tile_lds(f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split,
                                                uint32_t m0, uint32_t n0, int wave, int r, int g, float* stage) {
   constexpr int WN = 4 / WM, BN = 16 * FN * WN, LDR = BN + 4, CR = 64, BM = 16 * FM * WM;
   static_assert(WM == 1 || FN % 2 == 1, "2 x 2 layouts: SwiGLU handles one straddling pair (odd fragments per wave)");
@@ -107,11 +113,14 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; j += 2)
+      for (int j = 0; j < FN; j += 2) {
+        pin_acc(acc[i][j]);
+        pin_acc(acc[i][j + 1]);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           st[(i * 16 + 4 * g + e) * LDH + wave * 8 * FN + (j / 2) * 16 + r] =
               (_Float16)swiglu_f(acc[i][j][e], acc[i][j + 1][e]);
+      }
     __syncthreads();
     constexpr int OQ = OW / 8;  // 16-byte chunks per row
 #pragma unroll
@@ -152,10 +161,13 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
         static_for<0, (FN - J0) / 2>([&](auto qc) {
           constexpr int j = J0 + 2 * decltype(qc)::value;  // local pair (j, j + 1)
           constexpr int col = ((WNC * FN + j) / 2) * 16;
+          pin_acc(acc[i][j]);
+          pin_acc(acc[i][j + 1]);
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             st[(rbase + i * 16 + 4 * g + e) * LDH + col + r] = (_Float16)swiglu_f(acc[i][j][e], acc[i][j + 1][e]);
         });
+        pin_acc(acc[i][WNC == 0 ? FN - 1 : 0]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if constexpr (WNC == 0)
@@ -208,9 +220,11 @@ __device__ __forceinline__ void store_tile_lds(const f4 (&acc)[FM][FN], const Ti
       const int tr = rbase + 16 * i;  // fragments never straddle a CR boundary
       if (tr < c0 || tr >= c0 + CR) continue;
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j) {
+        pin_acc(acc[i][j]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) stage[(tr - c0 + 4 * g + e) * LDR + cbase + j * 16 + r] = acc[i][j][e];
+      }
     }
     __syncthreads();
     // SwiGLU reaches this path only as split-K partials (raw fp32; the reduce applies it).
@@ -613,7 +627,6 @@ void gemm_tile22_kernel(const TileArgs p) {
   X(10, 3, 3)           \
   X(12, 2, 3)           \
   X(13, 2, 3)           \
-  X(14, 2, 3)           \
   X(5, 3, 3)            \
   X(7, 3, 3)            \
   X(9, 3, 3)            \
@@ -629,6 +642,11 @@ static const VariantEntry kVariants[] = {
     DH_TILE_MENU(DH_TILE_ENTRY)
     // 160 x 288: at M ≈ 603 the gate|up projection is 4 x 64 = 256 tiles, one per CU
     {{5, 9, 2, 2}, gemm_tile22_kernel<5, 9, 2, 3>},
+    // 288 x 224 and 224 x 224: the M = 2307 projections in fewer rounds of 256 tiles
+    {{9, 7, 2, 2}, gemm_tile22_kernel<9, 7, 2, 3>},
+    {{7, 7, 2, 2}, gemm_tile22_kernel<7, 7, 2, 3>},
+    // 160 x 160: the N = 2560 projections (10 % less LDS traffic per output than 96 x 256)
+    {{5, 5, 2, 2}, gemm_tile22_kernel<5, 5, 3, 3>},
 };
 #undef DH_TILE_ENTRY
 

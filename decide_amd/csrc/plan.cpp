@@ -39,128 +39,129 @@ struct Measured {
 };
 
 // {k, n, m, variant, splits}: fastest on an MI355X (gfx950, 256 CUs), the
-// variant index into the compiled menu (gemm_tile.hip: FM 1, 2, 4, 6, 8, 10,
-// 12, 13, 14, 5, 7, 9, 11, then the 2 x 2 tile 160 x 288), weights rotated
-// over > 256 MB. Regenerate with
-// `python -m decide_amd.tune_gemm` after any change to the tile kernel.
+// variant index into the compiled menu (gemm_tile.hip: 4 waves in a row with
+// FM 1, 2, 4, 6, 8, 10, 12, 13, 5, 7, 9, 11, then the 2 x 2 tiles 160 x 288,
+// 288 x 224, 224 x 224 and 160 x 160), weights rotated over > 256 MB.
+// Regenerate with `python -m decide_amd.tune_gemm` after any change to the
+// tile kernel.
 const Measured kMeasured[] = {
-    {2560, 12352, 1, 0, 4},  // 16.37 us
-    {2560, 12352, 3, 0, 4},  // 16.98 us
-    {2560, 12352, 8, 0, 4},  // 16.83 us
-    {2560, 12352, 16, 0, 4},  // 17.39 us
-    {2560, 12352, 24, 1, 4},  // 18.04 us
-    {2560, 12352, 48, 2, 4},  // 20.25 us
-    {2560, 12352, 96, 3, 4},  // 24.65 us
-    {2560, 12352, 163, 10, 2},  // 31.3 us
-    {2560, 12352, 276, 2, 1},  // 35.73 us
-    {2560, 12352, 490, 10, 1},  // 44.69 us
-    {2560, 12352, 603, 4, 1},  // 47.89 us
-    {2560, 12352, 1024, 7, 1},  // 67.67 us
-    {2560, 12352, 2307, 5, 1},  // 157.29 us
-    {2560, 10240, 1, 0, 4},  // 15.07 us
-    {2560, 10240, 3, 1, 4},  // 15.65 us
-    {2560, 10240, 8, 0, 4},  // 15.68 us
-    {2560, 10240, 16, 0, 4},  // 16.13 us
-    {2560, 10240, 24, 1, 4},  // 17.01 us
-    {2560, 10240, 48, 2, 4},  // 18.98 us
-    {2560, 10240, 96, 1, 2},  // 22.51 us
-    {2560, 10240, 163, 2, 2},  // 26.28 us
-    {2560, 10240, 276, 3, 2},  // 32.29 us
-    {2560, 10240, 490, 3, 1},  // 39.38 us
-    {2560, 10240, 603, 10, 1},  // 43.38 us
-    {2560, 10240, 1024, 12, 1},  // 58.49 us
-    {2560, 10240, 2307, 7, 1},  // 131.46 us
-    {2560, 18432, 1, 0, 3},  // 21.61 us
-    {2560, 18432, 3, 0, 3},  // 21.74 us
-    {2560, 18432, 8, 0, 3},  // 22.06 us
-    {2560, 18432, 16, 0, 3},  // 22.64 us
-    {2560, 18432, 24, 1, 3},  // 23.59 us
-    {2560, 18432, 48, 9, 3},  // 26.43 us
-    {2560, 18432, 96, 12, 3},  // 32.55 us
-    {2560, 18432, 163, 2, 1},  // 35.71 us
-    {2560, 18432, 276, 3, 1},  // 40.14 us
-    {2560, 18432, 490, 12, 1},  // 50.69 us
-    {2560, 18432, 603, 13, 1},  // 54.81 us
-    {2560, 18432, 1024, 5, 1},  // 90.08 us
-    {2560, 18432, 2307, 12, 1},  // 201.23 us
-    {4096, 2560, 1, 0, 6},  // 11.41 us
-    {4096, 2560, 3, 0, 8},  // 11.82 us
-    {4096, 2560, 8, 0, 6},  // 12.32 us
-    {4096, 2560, 16, 1, 6},  // 12.84 us
-    {4096, 2560, 24, 0, 8},  // 12.88 us
-    {4096, 2560, 48, 0, 6},  // 13.87 us
-    {4096, 2560, 96, 1, 8},  // 15.44 us
-    {4096, 2560, 163, 1, 4},  // 17.56 us
-    {4096, 2560, 276, 9, 6},  // 19.85 us
-    {4096, 2560, 490, 3, 4},  // 24.16 us
-    {4096, 2560, 603, 10, 4},  // 26.87 us
-    {4096, 2560, 1024, 4, 3},  // 36.27 us
-    {4096, 2560, 2307, 3, 1},  // 58.95 us
-    {9216, 2560, 1, 0, 8},  // 19.39 us
-    {9216, 2560, 3, 0, 8},  // 19.55 us
-    {9216, 2560, 8, 0, 8},  // 19.95 us
-    {9216, 2560, 16, 0, 8},  // 20.44 us
-    {9216, 2560, 24, 0, 8},  // 20.78 us
-    {9216, 2560, 48, 0, 8},  // 20.87 us
-    {9216, 2560, 96, 1, 8},  // 22.4 us
-    {9216, 2560, 163, 2, 8},  // 24.71 us
-    {9216, 2560, 276, 3, 8},  // 28.55 us
-    {9216, 2560, 490, 4, 6},  // 36.6 us
-    {9216, 2560, 603, 10, 4},  // sustained bench loop (gate|up + down): 103.9 us per step against 106.6 for (5, 6), the burst best
-    {9216, 2560, 1024, 4, 3},  // 57.89 us
-    {9216, 2560, 2307, 3, 1},  // 116.32 us
-    {2560, 2048, 1, 0, 6},  // 10.06 us
-    {2560, 2048, 3, 0, 6},  // 10.23 us
-    {2560, 2048, 8, 0, 6},  // 10.61 us
-    {2560, 2048, 16, 0, 4},  // 10.8 us
-    {2560, 2048, 24, 0, 4},  // 10.99 us
-    {2560, 2048, 48, 0, 4},  // 11.27 us
-    {2560, 2048, 96, 0, 4},  // 11.67 us
-    {2560, 2048, 163, 1, 4},  // 13.15 us
-    {2560, 2048, 276, 2, 3},  // 15.83 us
-    {2560, 2048, 490, 2, 4},  // 16.72 us
-    {2560, 2048, 603, 2, 3},  // 17.93 us
-    {2560, 2048, 1024, 2, 2},  // 22.5 us
-    {2560, 2048, 2307, 3, 1},  // 33.38 us
-    {2560, 8192, 1, 0, 6},  // 13.97 us
-    {2560, 8192, 3, 0, 6},  // 14.18 us
-    {2560, 8192, 8, 0, 4},  // 14.62 us
-    {2560, 8192, 16, 0, 6},  // 15.0 us
-    {2560, 8192, 24, 0, 4},  // 15.22 us
-    {2560, 8192, 48, 1, 4},  // 16.33 us
-    {2560, 8192, 96, 2, 4},  // 18.92 us
-    {2560, 8192, 163, 3, 4},  // 24.05 us
-    {2560, 8192, 276, 9, 2},  // 28.71 us
-    {2560, 8192, 490, 2, 1},  // 35.73 us
-    {2560, 8192, 603, 3, 1},  // 39.32 us
-    {2560, 8192, 1024, 4, 1},  // 47.95 us
-    {2560, 8192, 2307, 5, 1},  // 104.01 us
-    {2560, 6144, 1, 0, 6},  // 13.03 us
-    {2560, 6144, 3, 0, 6},  // 13.27 us
-    {2560, 6144, 8, 0, 6},  // 13.73 us
-    {2560, 6144, 16, 0, 8},  // 14.19 us
-    {2560, 6144, 24, 0, 4},  // 14.53 us
-    {2560, 6144, 48, 1, 4},  // 15.63 us
-    {2560, 6144, 96, 2, 4},  // 17.86 us
-    {2560, 6144, 163, 2, 3},  // 21.06 us
-    {2560, 6144, 276, 2, 2},  // 24.82 us
-    {2560, 6144, 490, 10, 2},  // 32.39 us
-    {2560, 6144, 603, 2, 1},  // 34.7 us
-    {2560, 6144, 1024, 10, 1},  // 42.45 us
-    {2560, 6144, 2307, 4, 1},  // 88.02 us
-    {2560, 9216, 1, 0, 4},  // 14.49 us
-    {2560, 9216, 3, 0, 4},  // 14.66 us
-    {2560, 9216, 8, 0, 4},  // 15.05 us
-    {2560, 9216, 16, 0, 6},  // 15.51 us
-    {2560, 9216, 24, 0, 3},  // 17.05 us
-    {2560, 9216, 48, 2, 4},  // 18.27 us
-    {2560, 9216, 96, 2, 3},  // 21.76 us
-    {2560, 9216, 163, 2, 2},  // 25.15 us
-    {2560, 9216, 276, 3, 2},  // 30.91 us
-    {2560, 9216, 490, 9, 1},  // 38.08 us
-    {2560, 9216, 603, 3, 1},  // 39.9 us
-    {2560, 9216, 1024, 5, 1},  // 53.39 us
-    {2560, 9216, 2307, 12, 1},  // 116.93 us
+    {2560, 12352, 1, 0, 4},  // 16.73 us
+    {2560, 12352, 3, 0, 4},  // 16.71 us
+    {2560, 12352, 8, 0, 4},  // 17.35 us
+    {2560, 12352, 16, 0, 4},  // 17.6 us
+    {2560, 12352, 24, 1, 4},  // 18.32 us
+    {2560, 12352, 48, 2, 4},  // 20.51 us
+    {2560, 12352, 96, 15, 3},  // 25.0 us
+    {2560, 12352, 163, 4, 2},  // 31.97 us
+    {2560, 12352, 276, 2, 1},  // 37.09 us
+    {2560, 12352, 490, 9, 1},  // 44.02 us
+    {2560, 12352, 603, 4, 1},  // 47.8 us
+    {2560, 12352, 1024, 7, 1},  // 66.88 us
+    {2560, 12352, 2307, 5, 1},  // 153.8 us
+    {2560, 10240, 1, 0, 4},  // 15.59 us
+    {2560, 10240, 3, 0, 4},  // 15.65 us
+    {2560, 10240, 8, 0, 4},  // 16.18 us
+    {2560, 10240, 16, 0, 4},  // 16.83 us
+    {2560, 10240, 24, 1, 4},  // 17.22 us
+    {2560, 10240, 48, 2, 4},  // 19.63 us
+    {2560, 10240, 96, 15, 4},  // 21.74 us
+    {2560, 10240, 163, 15, 2},  // 27.07 us
+    {2560, 10240, 276, 15, 2},  // 31.77 us
+    {2560, 10240, 490, 15, 1},  // 37.61 us
+    {2560, 10240, 603, 15, 1},  // 40.8 us
+    {2560, 10240, 1024, 11, 1},  // 57.74 us
+    {2560, 10240, 2307, 14, 1},  // 127.31 us
+    {2560, 18432, 1, 0, 3},  // 22.01 us
+    {2560, 18432, 3, 0, 3},  // 22.21 us
+    {2560, 18432, 8, 0, 3},  // 22.56 us
+    {2560, 18432, 16, 1, 3},  // 23.31 us
+    {2560, 18432, 24, 1, 3},  // 23.92 us
+    {2560, 18432, 48, 8, 3},  // 27.41 us
+    {2560, 18432, 96, 15, 2},  // 30.72 us
+    {2560, 18432, 163, 15, 1},  // 33.34 us
+    {2560, 18432, 276, 15, 1},  // 38.12 us
+    {2560, 18432, 490, 11, 1},  // 50.06 us
+    {2560, 18432, 603, 12, 1},  // 54.16 us
+    {2560, 18432, 1024, 5, 1},  // 89.3 us
+    {2560, 18432, 2307, 11, 1},  // 201.87 us
+    {4096, 2560, 1, 0, 8},  // 12.94 us
+    {4096, 2560, 3, 0, 8},  // 13.15 us
+    {4096, 2560, 8, 0, 8},  // 13.58 us
+    {4096, 2560, 16, 0, 8},  // 13.94 us
+    {4096, 2560, 24, 0, 8},  // 14.07 us
+    {4096, 2560, 48, 0, 8},  // 14.62 us
+    {4096, 2560, 96, 1, 6},  // 15.94 us
+    {4096, 2560, 163, 2, 6},  // 18.35 us
+    {4096, 2560, 276, 2, 4},  // 20.55 us
+    {4096, 2560, 490, 3, 4},  // 24.61 us
+    {4096, 2560, 603, 15, 4},  // 26.63 us
+    {4096, 2560, 1024, 15, 2},  // 35.89 us
+    {4096, 2560, 2307, 15, 1},  // 58.37 us
+    {9216, 2560, 1, 0, 8},  // 20.5 us
+    {9216, 2560, 3, 0, 8},  // 20.81 us
+    {9216, 2560, 8, 0, 8},  // 21.55 us
+    {9216, 2560, 16, 0, 8},  // 21.93 us
+    {9216, 2560, 24, 0, 8},  // 21.95 us
+    {9216, 2560, 48, 0, 8},  // 21.89 us
+    {9216, 2560, 96, 1, 8},  // 23.35 us
+    {9216, 2560, 163, 2, 8},  // 25.63 us
+    {9216, 2560, 276, 15, 8},  // 29.42 us
+    {9216, 2560, 490, 4, 6},  // 37.65 us
+    {9216, 2560, 603, 15, 4},  // 40.85 us; also the best in the bench's sustained gate|up + down loop
+    {9216, 2560, 1024, 4, 3},  // 58.74 us
+    {9216, 2560, 2307, 15, 1},  // 109.81 us
+    {2560, 2048, 1, 0, 8},  // 11.54 us
+    {2560, 2048, 3, 0, 8},  // 11.75 us
+    {2560, 2048, 8, 0, 8},  // 12.14 us
+    {2560, 2048, 16, 0, 8},  // 12.46 us
+    {2560, 2048, 24, 0, 8},  // 12.52 us
+    {2560, 2048, 48, 0, 8},  // 12.71 us
+    {2560, 2048, 96, 1, 6},  // 14.0 us
+    {2560, 2048, 163, 1, 4},  // 14.73 us
+    {2560, 2048, 276, 1, 3},  // 17.57 us
+    {2560, 2048, 490, 2, 4},  // 20.41 us
+    {2560, 2048, 603, 2, 3},  // 21.8 us
+    {2560, 2048, 1024, 2, 2},  // 26.38 us
+    {2560, 2048, 2307, 15, 1},  // 37.54 us
+    {2560, 8192, 1, 0, 6},  // 14.42 us
+    {2560, 8192, 3, 0, 6},  // 14.66 us
+    {2560, 8192, 8, 0, 6},  // 15.07 us
+    {2560, 8192, 16, 0, 6},  // 15.22 us
+    {2560, 8192, 24, 0, 4},  // 15.56 us
+    {2560, 8192, 48, 1, 4},  // 16.82 us
+    {2560, 8192, 96, 2, 4},  // 19.5 us
+    {2560, 8192, 163, 3, 4},  // 23.27 us
+    {2560, 8192, 276, 8, 2},  // 29.28 us
+    {2560, 8192, 490, 15, 1},  // 36.12 us
+    {2560, 8192, 603, 3, 1},  // 40.13 us
+    {2560, 8192, 1024, 4, 1},  // 47.75 us
+    {2560, 8192, 2307, 5, 1},  // 103.75 us
+    {2560, 6144, 1, 0, 6},  // 13.28 us
+    {2560, 6144, 3, 0, 6},  // 13.51 us
+    {2560, 6144, 8, 0, 6},  // 13.99 us
+    {2560, 6144, 16, 0, 6},  // 14.38 us
+    {2560, 6144, 24, 1, 6},  // 14.97 us
+    {2560, 6144, 48, 2, 8},  // 17.03 us
+    {2560, 6144, 96, 2, 4},  // 18.59 us
+    {2560, 6144, 163, 3, 4},  // 21.94 us
+    {2560, 6144, 276, 15, 3},  // 25.54 us
+    {2560, 6144, 490, 9, 2},  // 32.78 us
+    {2560, 6144, 603, 2, 1},  // 35.95 us
+    {2560, 6144, 1024, 9, 1},  // 41.85 us
+    {2560, 6144, 2307, 13, 1},  // 80.78 us
+    {2560, 9216, 1, 0, 6},  // 14.84 us
+    {2560, 9216, 3, 0, 6},  // 15.05 us
+    {2560, 9216, 8, 0, 4},  // 15.74 us
+    {2560, 9216, 16, 0, 6},  // 15.94 us
+    {2560, 9216, 24, 1, 4},  // 16.83 us
+    {2560, 9216, 48, 8, 6},  // 18.77 us
+    {2560, 9216, 96, 15, 4},  // 21.22 us
+    {2560, 9216, 163, 2, 2},  // 26.34 us
+    {2560, 9216, 276, 15, 2},  // 30.97 us
+    {2560, 9216, 490, 15, 1},  // 36.6 us
+    {2560, 9216, 603, 15, 1},  // 40.48 us
+    {2560, 9216, 1024, 5, 1},  // 52.6 us
+    {2560, 9216, 2307, 11, 1},  // 113.15 us
 };
 }  // namespace
 
@@ -263,9 +264,36 @@ Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws
   return plan_model(m, n, k, epi, max_ws);
 }
 
-Plan plan_grouped(uint32_t m, uint32_t n_total, uint32_t k) {
-  // Members share X and launch together; plan as one GEMM of the summed width.
-  return plan_gemm(m, n_total, k, 0u, 0);
+Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count) {
+  // Members share X and launch together: plan as one GEMM of the summed width
+  // (the table's row for that width is measured on the grouped launch where
+  // the engine has one), unless the members' own stripe rounding would add a
+  // round of 256 tiles to that plan; then the model picks, counting the
+  // stripes member by member.
+  uint32_t n_total = 0;
+  for (uint32_t i = 0; i < count; ++i) n_total += ns[i];
+  const Plan p = plan_gemm(m, n_total, k, 0u, 0);
+  if (p.variant == kStreamVariant) return p;
+  // the width whose single-GEMM stripe count equals the grouped one for variant v
+  auto grouped_n = [&](int v) {
+    const uint32_t bn = (uint32_t)variant_info(v).bn();
+    uint32_t s = 0;
+    for (uint32_t i = 0; i < count; ++i) s += ceil_div(ns[i], bn);
+    return s * bn;
+  };
+  const uint32_t cus = (uint32_t)kCUs;
+  const uint32_t bn = (uint32_t)variant_info(p.variant).bn();
+  if (ceil_div(p.mtiles * (grouped_n(p.variant) / bn), cus) <= ceil_div(p.grid, cus)) return p;
+  Plan best = p;
+  double best_us = std::numeric_limits<double>::infinity();
+  for (int v = 0; v < variant_count(); ++v) {
+    const double t = plan_estimate_us(v, 1, m, grouped_n(v), k, 0u);
+    if (t < best_us) {
+      best_us = t;
+      best = plan_make(v, 1, m, n_total, k, 0u);
+    }
+  }
+  return best;
 }
 
 }  // namespace dh

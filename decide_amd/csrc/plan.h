@@ -39,7 +39,8 @@ Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k,
 Plan plan_stream(uint32_t m, uint32_t n, uint32_t k, uint64_t max_ws);
 // Best plan for a single GEMM. `max_ws` caps the split-K workspace bytes.
 Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws);
-// Best plan for a grouped launch of total width n_total (no split-K).
-Plan plan_grouped(uint32_t m, uint32_t n_total, uint32_t k);
+// Best plan for a grouped launch of `count` members of widths ns[] that share
+// X (no split-K). Each member rounds up to whole column stripes of its own.
+Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count);
 
 }  // namespace dh

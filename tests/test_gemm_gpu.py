@@ -308,6 +308,25 @@ def test_config3_grouped_projections_m603(gpu, kernels, stream, group):
     check_gemm(f"C3 {group} out", to_host(res)[rows] - x0[rows], want)
 
 
+def test_grouped_qkv_m2307_member_stripes(gpu, kernels, stream):
+    """BASELINE's Q|K|V group at M = 2307: its members round up to whole column stripes each, which for
+    the single-GEMM choice at N = 6144 would add a round of tiles, so the grouped planner re-plans; the
+    re-planned launch still matches the oracle on every member (sampled rows)."""
+    m, d, widths = 2307, 2560, [4096, 1024, 1024]
+    x = synth.normal_f16(synth.seed_for(33), (m, d), 1.0)
+    ws = [synth.normal_f16(synth.seed_for(43 + i), (n, d), 0.02) for i, n in enumerate(widths)]
+    ys = [full((m, n), np.float32, np.nan) for n in widths]
+    members = [((to_dev(w), 0), d, n, (y, 0), n, Epilogue.StoreF32) for w, n, y in zip(ws, widths, ys)]
+    kernels.gemm.gemm_grouped(stream, (to_dev(x), 0), d, m, d, members)
+    sync()
+    rows = sample_rows(m)
+    for i, (w, y) in enumerate(zip(ws, ys)):
+        got = to_host(y)
+        assert np.isfinite(got).all(), f"member {i}: rows left unwritten"
+        want = orc.gemm_nt_f16(x, w, rows=rows)
+        check_gemm(f"Q|K|V m2307 member {i}", got[rows], want)
+        orc.assert_close(f"Q|K|V m2307 member {i}", got[rows], want, 1e-4, 1e-4)
+
 def test_grouped_equals_fused_single_gemm(gpu, kernels, stream):
     """A grouped launch over [W_a; W_b] gives the same bits as one GEMM over the concatenated rows when
     both use the same tile variant (decide fuses by concatenation, convert.rs:204-245)."""
