@@ -617,6 +617,16 @@ void gemm_tile22_kernel(const TileArgs p) {
   tile_body<FM, FN, 2, NBX, NBW>(p);
 }
 
+// Two workgroups per CU (two waves per SIMD): at most 256 registers per lane
+// and 80 KB of LDS each, so one workgroup's stage barriers and LDS waits
+// overlap the other's MFMAs.
+template <int FM, int FN, int WM, int NBX, int NBW>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
+void gemm_tile_o2_kernel(const TileArgs p) {
+  static_assert(Pipe<FM, FN, WM, NBX, NBW>::LDS_BYTES <= 80 * 1024, "two workgroups per CU");
+  tile_body<FM, FN, WM, NBX, NBW>(p);
+}
+
 // ---- the compiled menu: (FM, NBX, NBW). BM = 16·FM rows, BN = 256.
 #define DH_TILE_MENU(X) \
   X(1, 3, 3)            \
@@ -625,11 +635,9 @@ void gemm_tile22_kernel(const TileArgs p) {
   X(6, 3, 3)            \
   X(8, 3, 3)            \
   X(10, 3, 3)           \
-  X(12, 2, 3)           \
   X(13, 2, 3)           \
   X(5, 3, 3)            \
   X(7, 3, 3)            \
-  X(9, 3, 3)            \
   X(11, 2, 3)
 
 struct VariantEntry {
@@ -640,6 +648,8 @@ struct VariantEntry {
 #define DH_TILE_ENTRY(FM, NBX, NBW) {{FM, 4, 4, 1}, gemm_tile_kernel<FM, NBX, NBW>},
 static const VariantEntry kVariants[] = {
     DH_TILE_MENU(DH_TILE_ENTRY)
+    // 128 x 96, two per CU: small and medium M over narrow N
+    {{4, 3, 2, 2}, gemm_tile_o2_kernel<4, 3, 2, 2, 3>},
     // 160 x 288: at M ≈ 603 the gate|up projection is 4 x 64 = 256 tiles, one per CU
     {{5, 9, 2, 2}, gemm_tile22_kernel<5, 9, 2, 3>},
     // 288 x 224 and 224 x 224: the M = 2307 projections in fewer rounds of 256 tiles

@@ -40,128 +40,129 @@ struct Measured {
 
 // {k, n, m, variant, splits}: fastest on an MI355X (gfx950, 256 CUs), the
 // variant index into the compiled menu (gemm_tile.hip: 4 waves in a row with
-// FM 1, 2, 4, 6, 8, 10, 12, 13, 5, 7, 9, 11, then the 2 x 2 tiles 160 x 288,
-// 288 x 224, 224 x 224 and 160 x 160), weights rotated over > 256 MB.
+// FM 1, 2, 4, 6, 8, 10, 13, 5, 7, 11; the 2 x 2 tile 128 x 96 run two per
+// CU; then the 2 x 2 tiles 160 x 288, 288 x 224, 224 x 224 and 160 x 160),
+// weights rotated over > 256 MB.
 // Regenerate with `python -m decide_amd.tune_gemm` after any change to the
 // tile kernel.
 const Measured kMeasured[] = {
-    {2560, 12352, 1, 0, 4},  // 16.73 us
-    {2560, 12352, 3, 0, 4},  // 16.71 us
-    {2560, 12352, 8, 0, 4},  // 17.35 us
-    {2560, 12352, 16, 0, 4},  // 17.6 us
-    {2560, 12352, 24, 1, 4},  // 18.32 us
-    {2560, 12352, 48, 2, 4},  // 20.51 us
-    {2560, 12352, 96, 15, 3},  // 25.0 us
-    {2560, 12352, 163, 4, 2},  // 31.97 us
-    {2560, 12352, 276, 2, 1},  // 37.09 us
-    {2560, 12352, 490, 9, 1},  // 44.02 us
-    {2560, 12352, 603, 4, 1},  // 47.8 us
-    {2560, 12352, 1024, 7, 1},  // 66.88 us
-    {2560, 12352, 2307, 5, 1},  // 153.8 us
-    {2560, 10240, 1, 0, 4},  // 15.59 us
-    {2560, 10240, 3, 0, 4},  // 15.65 us
-    {2560, 10240, 8, 0, 4},  // 16.18 us
-    {2560, 10240, 16, 0, 4},  // 16.83 us
-    {2560, 10240, 24, 1, 4},  // 17.22 us
-    {2560, 10240, 48, 2, 4},  // 19.63 us
-    {2560, 10240, 96, 15, 4},  // 21.74 us
-    {2560, 10240, 163, 15, 2},  // 27.07 us
-    {2560, 10240, 276, 15, 2},  // 31.77 us
-    {2560, 10240, 490, 15, 1},  // 37.61 us
-    {2560, 10240, 603, 15, 1},  // 40.8 us
-    {2560, 10240, 1024, 11, 1},  // 57.74 us
-    {2560, 10240, 2307, 14, 1},  // 127.31 us
-    {2560, 18432, 1, 0, 3},  // 22.01 us
-    {2560, 18432, 3, 0, 3},  // 22.21 us
-    {2560, 18432, 8, 0, 3},  // 22.56 us
-    {2560, 18432, 16, 1, 3},  // 23.31 us
-    {2560, 18432, 24, 1, 3},  // 23.92 us
-    {2560, 18432, 48, 8, 3},  // 27.41 us
-    {2560, 18432, 96, 15, 2},  // 30.72 us
-    {2560, 18432, 163, 15, 1},  // 33.34 us
-    {2560, 18432, 276, 15, 1},  // 38.12 us
-    {2560, 18432, 490, 11, 1},  // 50.06 us
-    {2560, 18432, 603, 12, 1},  // 54.16 us
-    {2560, 18432, 1024, 5, 1},  // 89.3 us
-    {2560, 18432, 2307, 11, 1},  // 201.87 us
-    {4096, 2560, 1, 0, 8},  // 12.94 us
-    {4096, 2560, 3, 0, 8},  // 13.15 us
-    {4096, 2560, 8, 0, 8},  // 13.58 us
-    {4096, 2560, 16, 0, 8},  // 13.94 us
-    {4096, 2560, 24, 0, 8},  // 14.07 us
-    {4096, 2560, 48, 0, 8},  // 14.62 us
-    {4096, 2560, 96, 1, 6},  // 15.94 us
-    {4096, 2560, 163, 2, 6},  // 18.35 us
-    {4096, 2560, 276, 2, 4},  // 20.55 us
-    {4096, 2560, 490, 3, 4},  // 24.61 us
-    {4096, 2560, 603, 15, 4},  // 26.63 us
-    {4096, 2560, 1024, 15, 2},  // 35.89 us
-    {4096, 2560, 2307, 15, 1},  // 58.37 us
-    {9216, 2560, 1, 0, 8},  // 20.5 us
-    {9216, 2560, 3, 0, 8},  // 20.81 us
-    {9216, 2560, 8, 0, 8},  // 21.55 us
-    {9216, 2560, 16, 0, 8},  // 21.93 us
-    {9216, 2560, 24, 0, 8},  // 21.95 us
-    {9216, 2560, 48, 0, 8},  // 21.89 us
-    {9216, 2560, 96, 1, 8},  // 23.35 us
-    {9216, 2560, 163, 2, 8},  // 25.63 us
-    {9216, 2560, 276, 15, 8},  // 29.42 us
-    {9216, 2560, 490, 4, 6},  // 37.65 us
-    {9216, 2560, 603, 15, 4},  // 40.85 us; also the best in the bench's sustained gate|up + down loop
-    {9216, 2560, 1024, 4, 3},  // 58.74 us
-    {9216, 2560, 2307, 15, 1},  // 109.81 us
-    {2560, 2048, 1, 0, 8},  // 11.54 us
-    {2560, 2048, 3, 0, 8},  // 11.75 us
-    {2560, 2048, 8, 0, 8},  // 12.14 us
-    {2560, 2048, 16, 0, 8},  // 12.46 us
-    {2560, 2048, 24, 0, 8},  // 12.52 us
-    {2560, 2048, 48, 0, 8},  // 12.71 us
-    {2560, 2048, 96, 1, 6},  // 14.0 us
-    {2560, 2048, 163, 1, 4},  // 14.73 us
-    {2560, 2048, 276, 1, 3},  // 17.57 us
-    {2560, 2048, 490, 2, 4},  // 20.41 us
-    {2560, 2048, 603, 2, 3},  // 21.8 us
-    {2560, 2048, 1024, 2, 2},  // 26.38 us
-    {2560, 2048, 2307, 15, 1},  // 37.54 us
-    {2560, 8192, 1, 0, 6},  // 14.42 us
-    {2560, 8192, 3, 0, 6},  // 14.66 us
-    {2560, 8192, 8, 0, 6},  // 15.07 us
+    {2560, 12352, 1, 0, 4},  // 16.93 us
+    {2560, 12352, 3, 0, 4},  // 17.38 us
+    {2560, 12352, 8, 0, 4},  // 17.1 us
+    {2560, 12352, 16, 0, 4},  // 17.62 us
+    {2560, 12352, 24, 1, 4},  // 18.45 us
+    {2560, 12352, 48, 2, 4},  // 20.74 us
+    {2560, 12352, 96, 3, 4},  // 25.04 us
+    {2560, 12352, 163, 3, 2},  // 32.33 us
+    {2560, 12352, 276, 2, 1},  // 37.29 us
+    {2560, 12352, 490, 8, 1},  // 44.58 us
+    {2560, 12352, 603, 4, 1},  // 48.23 us
+    {2560, 12352, 1024, 6, 1},  // 69.78 us
+    {2560, 12352, 2307, 5, 1},  // 154.67 us
+    {2560, 10240, 1, 0, 4},  // 15.58 us
+    {2560, 10240, 3, 0, 4},  // 15.75 us
+    {2560, 10240, 8, 0, 4},  // 16.12 us
+    {2560, 10240, 16, 0, 4},  // 16.91 us
+    {2560, 10240, 24, 1, 4},  // 17.18 us
+    {2560, 10240, 48, 2, 4},  // 19.66 us
+    {2560, 10240, 96, 10, 2},  // 22.46 us
+    {2560, 10240, 163, 2, 2},  // 27.17 us
+    {2560, 10240, 276, 14, 2},  // 33.13 us
+    {2560, 10240, 490, 14, 1},  // 38.14 us
+    {2560, 10240, 603, 14, 1},  // 41.83 us
+    {2560, 10240, 1024, 9, 1},  // 58.53 us
+    {2560, 10240, 2307, 6, 1},  // 132.62 us
+    {2560, 18432, 1, 0, 3},  // 22.05 us
+    {2560, 18432, 3, 0, 3},  // 22.44 us
+    {2560, 18432, 8, 0, 3},  // 22.69 us
+    {2560, 18432, 16, 0, 3},  // 23.16 us
+    {2560, 18432, 24, 1, 3},  // 24.0 us
+    {2560, 18432, 48, 2, 3},  // 27.74 us
+    {2560, 18432, 96, 14, 2},  // 30.8 us
+    {2560, 18432, 163, 14, 1},  // 35.6 us
+    {2560, 18432, 276, 14, 1},  // 38.56 us
+    {2560, 18432, 490, 9, 1},  // 51.05 us
+    {2560, 18432, 603, 11, 1},  // 55.75 us
+    {2560, 18432, 1024, 5, 1},  // 92.78 us
+    {2560, 18432, 2307, 9, 1},  // 206.29 us
+    {4096, 2560, 1, 0, 8},  // 12.84 us
+    {4096, 2560, 3, 0, 8},  // 13.06 us
+    {4096, 2560, 8, 0, 8},  // 13.82 us
+    {4096, 2560, 16, 0, 8},  // 14.24 us
+    {4096, 2560, 24, 0, 8},  // 14.31 us
+    {4096, 2560, 48, 0, 6},  // 14.87 us
+    {4096, 2560, 96, 10, 6},  // 16.16 us
+    {4096, 2560, 163, 10, 4},  // 18.31 us
+    {4096, 2560, 276, 2, 4},  // 20.7 us
+    {4096, 2560, 490, 3, 4},  // 25.04 us
+    {4096, 2560, 603, 14, 4},  // 26.99 us
+    {4096, 2560, 1024, 14, 2},  // 37.01 us
+    {4096, 2560, 2307, 3, 1},  // 59.58 us
+    {9216, 2560, 1, 0, 8},  // 20.69 us
+    {9216, 2560, 3, 0, 8},  // 21.26 us
+    {9216, 2560, 8, 0, 8},  // 21.49 us
+    {9216, 2560, 16, 0, 8},  // 21.92 us
+    {9216, 2560, 24, 0, 8},  // 21.84 us
+    {9216, 2560, 48, 0, 8},  // 21.8 us
+    {9216, 2560, 96, 10, 8},  // 22.12 us
+    {9216, 2560, 163, 2, 8},  // 25.9 us
+    {9216, 2560, 276, 3, 8},  // 29.77 us
+    {9216, 2560, 490, 4, 6},  // 38.48 us
+    {9216, 2560, 603, 14, 4},  // 41.29 us; also the best in the bench's sustained gate|up + down loop
+    {9216, 2560, 1024, 4, 3},  // 60.08 us
+    {9216, 2560, 2307, 14, 1},  // 114.28 us
+    {2560, 2048, 1, 0, 6},  // 11.68 us
+    {2560, 2048, 3, 0, 6},  // 11.89 us
+    {2560, 2048, 8, 1, 8},  // 12.82 us
+    {2560, 2048, 16, 0, 8},  // 12.68 us
+    {2560, 2048, 24, 0, 8},  // 12.68 us
+    {2560, 2048, 48, 0, 8},  // 13.05 us
+    {2560, 2048, 96, 10, 6},  // 13.66 us
+    {2560, 2048, 163, 1, 4},  // 14.8 us
+    {2560, 2048, 276, 10, 4},  // 16.13 us
+    {2560, 2048, 490, 10, 2},  // 19.93 us
+    {2560, 2048, 603, 10, 2},  // 20.53 us
+    {2560, 2048, 1024, 8, 3},  // 26.57 us
+    {2560, 2048, 2307, 14, 1},  // 38.03 us
+    {2560, 8192, 1, 0, 6},  // 14.74 us
+    {2560, 8192, 3, 0, 6},  // 14.86 us
+    {2560, 8192, 8, 0, 6},  // 14.9 us
     {2560, 8192, 16, 0, 6},  // 15.22 us
-    {2560, 8192, 24, 0, 4},  // 15.56 us
-    {2560, 8192, 48, 1, 4},  // 16.82 us
-    {2560, 8192, 96, 2, 4},  // 19.5 us
-    {2560, 8192, 163, 3, 4},  // 23.27 us
-    {2560, 8192, 276, 8, 2},  // 29.28 us
-    {2560, 8192, 490, 15, 1},  // 36.12 us
-    {2560, 8192, 603, 3, 1},  // 40.13 us
-    {2560, 8192, 1024, 4, 1},  // 47.75 us
-    {2560, 8192, 2307, 5, 1},  // 103.75 us
-    {2560, 6144, 1, 0, 6},  // 13.28 us
-    {2560, 6144, 3, 0, 6},  // 13.51 us
-    {2560, 6144, 8, 0, 6},  // 13.99 us
-    {2560, 6144, 16, 0, 6},  // 14.38 us
+    {2560, 8192, 24, 0, 4},  // 15.63 us
+    {2560, 8192, 48, 1, 4},  // 16.9 us
+    {2560, 8192, 96, 2, 4},  // 20.22 us
+    {2560, 8192, 163, 3, 4},  // 23.86 us
+    {2560, 8192, 276, 7, 2},  // 29.5 us
+    {2560, 8192, 490, 14, 1},  // 36.56 us
+    {2560, 8192, 603, 3, 1},  // 40.52 us
+    {2560, 8192, 1024, 4, 1},  // 48.11 us
+    {2560, 8192, 2307, 5, 1},  // 104.84 us
+    {2560, 6144, 1, 0, 6},  // 13.27 us
+    {2560, 6144, 3, 0, 8},  // 13.73 us
+    {2560, 6144, 8, 0, 6},  // 14.02 us
+    {2560, 6144, 16, 0, 8},  // 14.41 us
     {2560, 6144, 24, 1, 6},  // 14.97 us
-    {2560, 6144, 48, 2, 8},  // 17.03 us
-    {2560, 6144, 96, 2, 4},  // 18.59 us
-    {2560, 6144, 163, 3, 4},  // 21.94 us
-    {2560, 6144, 276, 15, 3},  // 25.54 us
-    {2560, 6144, 490, 9, 2},  // 32.78 us
-    {2560, 6144, 603, 2, 1},  // 35.95 us
-    {2560, 6144, 1024, 9, 1},  // 41.85 us
-    {2560, 6144, 2307, 13, 1},  // 80.78 us
+    {2560, 6144, 48, 1, 4},  // 16.02 us
+    {2560, 6144, 96, 10, 4},  // 16.76 us
+    {2560, 6144, 163, 10, 2},  // 20.52 us
+    {2560, 6144, 276, 14, 3},  // 25.75 us
+    {2560, 6144, 490, 10, 1},  // 29.33 us
+    {2560, 6144, 603, 2, 1},  // 36.06 us
+    {2560, 6144, 1024, 8, 1},  // 42.61 us
+    {2560, 6144, 2307, 12, 1},  // 83.85 us
     {2560, 9216, 1, 0, 6},  // 14.84 us
-    {2560, 9216, 3, 0, 6},  // 15.05 us
-    {2560, 9216, 8, 0, 4},  // 15.74 us
-    {2560, 9216, 16, 0, 6},  // 15.94 us
-    {2560, 9216, 24, 1, 4},  // 16.83 us
-    {2560, 9216, 48, 8, 6},  // 18.77 us
-    {2560, 9216, 96, 15, 4},  // 21.22 us
-    {2560, 9216, 163, 2, 2},  // 26.34 us
-    {2560, 9216, 276, 15, 2},  // 30.97 us
-    {2560, 9216, 490, 15, 1},  // 36.6 us
-    {2560, 9216, 603, 15, 1},  // 40.48 us
-    {2560, 9216, 1024, 5, 1},  // 52.6 us
-    {2560, 9216, 2307, 11, 1},  // 113.15 us
+    {2560, 9216, 3, 0, 6},  // 15.19 us
+    {2560, 9216, 8, 0, 4},  // 15.68 us
+    {2560, 9216, 16, 0, 6},  // 15.84 us
+    {2560, 9216, 24, 1, 6},  // 16.8 us
+    {2560, 9216, 48, 7, 6},  // 18.91 us
+    {2560, 9216, 96, 14, 4},  // 21.41 us
+    {2560, 9216, 163, 2, 2},  // 26.37 us
+    {2560, 9216, 276, 14, 2},  // 30.9 us
+    {2560, 9216, 490, 14, 1},  // 37.03 us
+    {2560, 9216, 603, 14, 1},  // 40.99 us
+    {2560, 9216, 1024, 5, 1},  // 54.61 us
+    {2560, 9216, 2307, 9, 1},  // 116.58 us
 };
 }  // namespace
 
