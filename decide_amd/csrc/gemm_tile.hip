@@ -322,9 +322,12 @@ struct Pipe {
   static constexpr int XBYTES = XR * 128, WBYTES = BN * 128;
   static constexpr int WRING = NBX * XBYTES;  // offset of the W ring
   static constexpr int LDS_BYTES = NBX * XBYTES + NBW * WBYTES;
-  // outstanding DMAs allowed at the end of a stage (those not needed next)
-  static constexpr int KEEP = (LAX >= 2 ? XPW : 0) + (LAW >= 2 ? WPW : 0);
-  static_assert(NBX >= 2 && NBW >= 2 && NBX <= 3 && NBW <= 3, "ring depths 2 or 3");
+  // outstanding DMAs allowed at the end of a stage (those not needed next):
+  // with equal depths, the DMAs of stages kt + 2 .. kt + LA
+  static constexpr int KEEP = NBX == NBW ? (LAX - 1) * (XPW + WPW) : (LAX >= 2 ? XPW : 0) + (LAW >= 2 ? WPW : 0);
+  static_assert(NBX >= 2 && NBW >= 2 && ((NBX == NBW && NBX <= 5) || (NBX == 2 && NBW == 3)),
+                "ring depths: equal (2 to 5), or 2 for X and 3 for W");
+  static_assert(KEEP + XPW + WPW <= 63, "outstanding DMAs fit the vmcnt counter");
   static_assert((WM == 1 && FN == 4) || WM == 2, "wave layouts: 1 x 4 with 4 fragments per wave, or 2 x 2");
   static_assert(BN % 32 == 0, "whole 8-row DMA groups per wave");
 
@@ -446,6 +449,13 @@ struct Pipe {
       // DMAs still allowed in flight: this stage's issues not needed by stage kt + 1
       if (steady) {
         wait_vm<KEEP>();
+      } else if constexpr (NBX == NBW && NBX > 3) {
+        // near the end of K: the stages kt + 2 .. kt + LA that exist were issued
+        const int later = min(kt + LAX, nst - 1) - (kt + 1);
+        static_for<0, LAX>([&](auto cc) {
+          constexpr int c = decltype(cc)::value;
+          if (later == c) wait_vm<c * (XPW + WPW)>();
+        });
       } else {
         const bool ix2 = LAX >= 2 && kt + LAX < nst, iw2 = LAW >= 2 && kt + LAW < nst;
         if (ix2 && iw2)
@@ -527,25 +537,40 @@ __device__ __forceinline__ void tile_body(const TileArgs& p) {
     // prologue: X(0..LAX-1) and W(0..LAW-1) in flight; stage 0's land first.
     pp.template dma_x<0>(0);
     pp.template dma_w<0>(0);
-    int later = 0;  // DMAs issued after stage 0's
-    if (nst > 1) {
-      if (P::LAX >= 2) {
-        pp.template dma_x<1 % NBX>(1);
-        later += P::XPW;
+    if constexpr (NBX == NBW && NBX > 3) {
+      static_for<1, P::LAX>([&](auto sc) {
+        constexpr int st = decltype(sc)::value;
+        if (st < nst) {
+          pp.template dma_x<st>(st);
+          pp.template dma_w<st>(st);
+        }
+      });
+      const int later = min(P::LAX, nst) - 1;  // stages issued after stage 0
+      static_for<0, P::LAX>([&](auto cc) {
+        constexpr int c = decltype(cc)::value;
+        if (later == c) wait_vm<c * (P::XPW + P::WPW)>();
+      });
+    } else {
+      int later = 0;  // DMAs issued after stage 0's
+      if (nst > 1) {
+        if (P::LAX >= 2) {
+          pp.template dma_x<1 % NBX>(1);
+          later += P::XPW;
+        }
+        if (P::LAW >= 2) {
+          pp.template dma_w<1 % NBW>(1);
+          later += P::WPW;
+        }
       }
-      if (P::LAW >= 2) {
-        pp.template dma_w<1 % NBW>(1);
-        later += P::WPW;
-      }
+      if (later == P::XPW + P::WPW)
+        wait_vm<P::XPW + P::WPW>();
+      else if (later == P::XPW)
+        wait_vm<P::XPW>();
+      else if (later == P::WPW)
+        wait_vm<P::WPW>();
+      else
+        wait_vm<0>();
     }
-    if (later == P::XPW + P::WPW)
-      wait_vm<P::XPW + P::WPW>();
-    else if (later == P::XPW)
-      wait_vm<P::XPW>();
-    else if (later == P::WPW)
-      wait_vm<P::WPW>();
-    else
-      wait_vm<0>();
     __syncthreads();
 
     int kt = 0;
@@ -617,16 +642,6 @@ void gemm_tile22_kernel(const TileArgs p) {
   tile_body<FM, FN, 2, NBX, NBW>(p);
 }
 
-// Two workgroups per CU (two waves per SIMD): at most 256 registers per lane
-// and 80 KB of LDS each, so one workgroup's stage barriers and LDS waits
-// overlap the other's MFMAs.
-template <int FM, int FN, int WM, int NBX, int NBW>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
-void gemm_tile_o2_kernel(const TileArgs p) {
-  static_assert(Pipe<FM, FN, WM, NBX, NBW>::LDS_BYTES <= 80 * 1024, "two workgroups per CU");
-  tile_body<FM, FN, WM, NBX, NBW>(p);
-}
-
 // ---- the compiled menu: (FM, NBX, NBW). BM = 16·FM rows, BN = 256.
 #define DH_TILE_MENU(X) \
   X(1, 3, 3)            \
@@ -648,8 +663,8 @@ struct VariantEntry {
 #define DH_TILE_ENTRY(FM, NBX, NBW) {{FM, 4, 4, 1}, gemm_tile_kernel<FM, NBX, NBW>},
 static const VariantEntry kVariants[] = {
     DH_TILE_MENU(DH_TILE_ENTRY)
-    // 128 x 96, two per CU: small and medium M over narrow N
-    {{4, 3, 2, 2}, gemm_tile_o2_kernel<4, 3, 2, 2, 3>},
+    // 96 x 160 with a 5-deep ring: small M (48-96 rows) over wide N
+    {{3, 5, 2, 2}, gemm_tile22_kernel<3, 5, 5, 5>},
     // 160 x 288: at M ≈ 603 the gate|up projection is 4 x 64 = 256 tiles, one per CU
     {{5, 9, 2, 2}, gemm_tile22_kernel<5, 9, 2, 3>},
     // 288 x 224 and 224 x 224: the M = 2307 projections in fewer rounds of 256 tiles
@@ -657,6 +672,8 @@ static const VariantEntry kVariants[] = {
     {{7, 7, 2, 2}, gemm_tile22_kernel<7, 7, 2, 3>},
     // 160 x 160: the N = 2560 projections (10 % less LDS traffic per output than 96 x 256)
     {{5, 5, 2, 2}, gemm_tile22_kernel<5, 5, 3, 3>},
+    // 128 x 96 with a 5-deep ring: medium M (96-490 rows) over narrow N
+    {{4, 3, 2, 2}, gemm_tile22_kernel<4, 3, 5, 5>},
 };
 #undef DH_TILE_ENTRY
 
