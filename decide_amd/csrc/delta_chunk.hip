@@ -120,25 +120,27 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
                                                                const float* __restrict__ a_log,
                                                                const float* __restrict__ dt_bias, float* __restrict__ ws,
                                                                uint32_t T) {
+  // 74 KB of LDS, so two workgroups share a CU: Q is staged only for M = Q Kᵀ, and A and T then take its
+  // place; V never goes through LDS (each wave loads its U operand into registers during the inversion).
+  constexpr int kR2 = C * LDF > 2 * C * LDT ? C * LDF : 2 * C * LDT;
   __shared__ __attribute__((aligned(16))) float Ks[C * LDF];
-  __shared__ __attribute__((aligned(16))) float QVs[C * LDF];  // Q, then V
-  __shared__ __attribute__((aligned(16))) float As[C * LDT];
-  __shared__ __attribute__((aligned(16))) float Ts[C * LDT];
+  __shared__ __attribute__((aligned(16))) float R2[kR2];  // Q; then A | T
   __shared__ __attribute__((aligned(16))) float Lg[C], Bt[C], Gm[C], SCw[C], Rh[C];
   __shared__ float Ysc[4 * 16 * 17];  // per-wave 16 × 16 scratch of the blocked inversion
+  float* const Qs = R2;
+  float* const As = R2;
+  float* const Ts = R2 + C * LDT;
   const uint32_t c = blockIdx.x, h = blockIdx.y, hk = h >> 1, t0 = c * C;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   float* out = ws + ((size_t)c * NV + h) * kWsStride;
 
-  f4 xv[8];
-  {  // all loads in flight before the first LDS store; V waits in registers until Q is done
+  {  // all loads in flight before the first LDS store
     f4 xk[8], xq[8];
     fetch_rows(xk, k, t0, T, NK, hk, tid);
     fetch_rows(xq, q, t0, T, NK, hk, tid);
-    fetch_rows(xv, v, t0, T, NV, h, tid);
     stage_rows(Ks, xk, tid);
-    stage_rows(QVs, xq, tid);
+    stage_rows(Qs, xq, tid);
   }
   if (wave == 0) {
     const uint32_t t = t0 + lane;
@@ -162,13 +164,14 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
   }
   __syncthreads();
 
-  // K Kᵀ → A (strictly lower, β_i γ_i/γ_j), Q Kᵀ → M (lower incl. diagonal, γ_i/γ_j): the 2 × 10 blocks
-  // on or below the diagonal; M's blocks above it are written as zeros, A's are never read
+  // Q Kᵀ → M (lower incl. diagonal, γ_i/γ_j), then K Kᵀ → A (strictly lower, β_i γ_i/γ_j) over Q's LDS: the
+  // 10 blocks on or below the diagonal of each; M's blocks above it are written as zeros, A's are never read
   for (int tt = wave; tt < 20; tt += 4) {
-    const bool isq = tt >= 10;
+    const bool isq = tt < 10;
+    if (tt >= 10 && tt - 4 < 10) __syncthreads();  // every wave is past its last M block: Q is dead
     int ti, tj;
-    lower_block(isq ? tt - 10 : tt, ti, tj);
-    const f4 acc = nt_tile<DK>((isq ? QVs : Ks) + 16 * ti * LDF, LDF, Ks + 16 * tj * LDF, LDF, r, g,
+    lower_block(isq ? tt : tt - 10, ti, tj);
+    const f4 acc = nt_tile<DK>((isq ? Qs : Ks) + 16 * ti * LDF, LDF, Ks + 16 * tj * LDF, LDF, r, g,
                                f4{0.f, 0.f, 0.f, 0.f});
     const int j = 16 * tj + r;
 #pragma unroll
@@ -193,8 +196,19 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
     *(f4*)(out + kOffKt + d * C + j4) = x;
   }
   if (tid < C) out[kOffGam + tid] = Gm[tid];
-  __syncthreads();  // Q is done: V takes its place
-  stage_rows(QVs, xv, tid);
+
+  // This wave's U operand, V[t0 + 16 jb + 4 g + s][16 (2 wave + q2) + r], straight into registers; the loads
+  // run during the inversion below.
+  f4 vr[2][4];
+#pragma unroll
+  for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const uint32_t t = t0 + 16 * jb + 4 * g + s4;
+        vr[q2][jb][s4] = t < T ? v[((size_t)t * NV + h) * DV + 16 * (2 * wave + q2) + r] : 0.f;
+      }
 
   // T = (I + A)⁻¹, blocked 4 × 4 over 16 × 16 blocks. Diagonal blocks by forward
   // substitution (wave w, lane j < 16 owns column j of block w); then the
@@ -247,11 +261,10 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
 
   // W = T diag(βγ) K and U = T diag(β) V. Wave w: key/value columns 16 td for td = 2w, 2w + 1. T is lower
   // triangular, so row block ti sums over token blocks jb ≤ ti; within a block lane group g holds tokens
-  // 16 jb + 4 g .. + 4 (one ds_read_b128 of T and of the scale), and the B operand R[j][16 td + r] is
-  // conflict-free with the row stride of 132 floats.
+  // 16 jb + 4 g .. + 4 (one ds_read_b128 of T and of the scale), and the B operand K[j][16 td + r] is
+  // conflict-free with the row stride of 132 floats (V's comes from registers).
 #pragma unroll
   for (int isu = 0; isu < 2; ++isu) {
-    const float* R = isu ? QVs : Ks;
     const float* sc = isu ? Bt : SCw;
     float* dst = out + (isu ? kOffU : kOffW);
 #pragma unroll
@@ -264,8 +277,12 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
         for (int jb = 0; jb <= ti; ++jb) {
           ta[jb] = *(const f4*)(Ts + (16 * ti + r) * LDT + 16 * jb + 4 * g);
           sv[jb] = *(const f4*)(sc + 16 * jb + 4 * g);
+          if (isu) {
+            rb[jb] = vr[q2][jb];
+          } else {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) rb[jb][s] = R[(16 * jb + 4 * g + s) * LDF + d0 + r];
+            for (int s = 0; s < 4; ++s) rb[jb][s] = Ks[(16 * jb + 4 * g + s) * LDF + d0 + r];
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
         f4 acc = f4{0.f, 0.f, 0.f, 0.f};
