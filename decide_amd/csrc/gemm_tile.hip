@@ -7,10 +7,11 @@
 //
 //   * Workgroup = 4 wavefronts side by side along N, 64 columns each, every
 //     wave computing all BM = 16·FM rows of the tile with
-//     v_mfma_f32_16x16x32_f16 (BN = 256). One more variant arranges the
-//     4 waves 2 x 2 with 5 x 9 fragments each (160 x 288): at M ≈ 603 the
-//     gate|up projection then makes exactly one tile per CU, and each wave
-//     reads fewer LDS rows per MFMA (80 + 144 instead of 208 + 64).
+//     v_mfma_f32_16x16x32_f16 (BN = 256). The 2 x 2 variants arrange the
+//     4 waves 2 x 2 with FM x FN fragments each (32·FM x 32·FN tiles): each
+//     wave reads only half of the tile's X rows and half of its W rows from
+//     LDS, so LDS bytes per output fall with the tile's area; 160 x 288 makes
+//     exactly one gate|up tile per CU at M ≈ 603.
 //   * Both operands reach LDS by coalesced DMA (global_load_lds_dwordx4:
 //     eight lanes per 128-byte row segment, no VGPR staging). The MFMA B
 //     operand wants 16 different W rows per load instruction; gathered
@@ -21,9 +22,10 @@
 //     instruction writes 1 KB contiguously and the ds_read_b128 of 16
 //     consecutive rows spreads over all banks.
 //   * Rings of NBX X-tile and NBW W-tile stage buffers (W, the operand that
-//     streams from HBM, gets the deeper one). The DMAs the next stage needs
-//     are issued at the start of a stage, the rest are spread over its MFMAs;
-//     one vmcnt wait and one barrier end each stage.
+//     streams from HBM, gets the deeper one; small tiles, whose stages are
+//     short, take 5-deep rings so a DMA has several stages to land). The
+//     DMAs the next stage needs are issued at the start of a stage, the rest
+//     are spread over its MFMAs; one vmcnt wait and one barrier end each stage.
 //   * The hot loop (LDS reads two fragments ahead, MFMAs, waits, DMAs) is
 //     inline asm in program order: accumulators pinned in AGPRs so the
 //     register allocator cannot rotate them, and exact wait counts.
