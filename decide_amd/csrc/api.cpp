@@ -93,6 +93,11 @@ int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const v
   const uintptr_t y_align = (epi == DH_EPI_STORE_F32 || epi == DH_EPI_ADD_F32) ? 8 : 4;
   if (!aligned(y, y_align)) return fail(DH_EINVAL, "gemm (fast): y address %p must be a multiple of %u", y, (unsigned)y_align);
   if (!x || !w || !y) return fail(DH_EINVAL, "gemm: null operand");
+  // The tile kernel's DMA addresses a row as a 32-bit byte offset from the operand's base.
+  if ((uint64_t)(m - 1) * ldx * 2 + (uint64_t)k * 2 > UINT32_MAX)
+    return fail(DH_EINVAL, "gemm: X rows span more than 4 GiB (m = %u, ldx = %u); split the call along M", m, ldx);
+  if ((uint64_t)(n - 1) * ldw * 2 + (uint64_t)k * 2 > UINT32_MAX)
+    return fail(DH_EINVAL, "gemm: W rows span more than 4 GiB (n = %u, ldw = %u); split the call along N", n, ldw);
   return DH_OK;
 }
 

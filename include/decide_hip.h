@@ -100,7 +100,10 @@ uint32_t dh_variants_loaded(const dh_ctx* ctx);
  * fp32 accumulation, ldy in elements of y's type. Contract (gemm.rs:140-163):
  * n % 32 == 0, k % 32 == 0, m >= 1, ldx >= k, ldw >= k, ldy >= n (n/2 for
  * SwiGLU), ldx % 8 == 0, ldw % 8 == 0, ldy even, x and w 16-byte aligned, y
- * 8-byte (fp32 outputs) or 4-byte (fp16 outputs) aligned. */
+ * 8-byte (fp32 outputs) or 4-byte (fp16 outputs) aligned, and X's and W's rows
+ * each within 4 GiB of their base: ((m - 1)·ldx + k)·2 and ((n - 1)·ldw + k)·2
+ * at most 2^32 - 1 bytes (no such limit in decide; its engine shapes are far
+ * below it). */
 int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
                uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
 

@@ -59,6 +59,8 @@ def bad_gemm(**kw):
     (dict(y=4, epi=0), "multiple of 8"),
     (dict(y=2, epi=3, ldy=32), "multiple of 4"),
     (dict(epi=4), "epilogue"),
+    (dict(m=233017, ldx=9216, ldw=9216, k=9216), "X rows span more than 4 GiB"),
+    (dict(n=262144, ldx=8192, ldw=8192, ldy=262144, k=8192), "W rows span more than 4 GiB"),
 ])
 def test_gemm_contract_violations_are_rejected(kw, msg):
     rc, err = bad_gemm(**kw)
