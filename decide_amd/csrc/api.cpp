@@ -96,7 +96,7 @@ int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const v
   // The tile kernel's DMA addresses a row as a 32-bit byte offset from the operand's base.
   if ((uint64_t)(m - 1) * ldx * 2 + (uint64_t)k * 2 > UINT32_MAX)
     return fail(DH_EINVAL, "gemm: X rows span more than 4 GiB (m = %u, ldx = %u); split the call along M", m, ldx);
-  if ((uint64_t)(n - 1) * ldw * 2 + (uint64_t)k * 2 > UINT32_MAX)
+  if ((uint64_t)(n ? n - 1 : 0) * ldw * 2 + (uint64_t)k * 2 > UINT32_MAX)
     return fail(DH_EINVAL, "gemm: W rows span more than 4 GiB (n = %u, ldw = %u); split the call along N", n, ldw);
   return DH_OK;
 }
@@ -151,6 +151,7 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
     stripes += (mem[i].n + bn - 1) / bn;
   }
   a.nstripes = stripes;
+  if (stripes == 0) return ok();  // N = 0: nothing to compute
   if (p.splits > 1) {
     if (count != 1) return fail(DH_EINVAL, "gemm: split-K needs a single member");
     int rc = ensure_ws(c, p.ws_bytes);

@@ -780,6 +780,7 @@ __global__ void gemm_reference_kernel(const _Float16* __restrict__ x, uint32_t l
 hipError_t launch_gemm_reference(const _Float16* x, uint32_t ldx, const _Float16* w, uint32_t ldw, void* y,
                                  uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi, hipStream_t s) {
   const uint32_t ncols = epi == 3u ? n / 2 : n;
+  if (ncols == 0) return hipSuccess;
   hipLaunchKernelGGL(gemm_reference_kernel, dim3((ncols + 127) / 128, std::min<uint32_t>(m, 4096)), dim3(128), 0, s, x, ldx, w, ldw, y, ldy, m,
                      n, k, epi);
   return hipGetLastError();

@@ -175,9 +175,9 @@ Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k,
   Plan p{};
   p.variant = variant;
   const uint32_t stages = ceil_div(k, kBK);
-  splits = std::max(1u, std::min(splits, stages));
+  splits = std::max(1u, std::min(splits, std::max(stages, 1u)));
   p.kps = ceil_div(stages, splits) * kBK;
-  p.splits = ceil_div(k, p.kps);  // splits that would be empty are dropped
+  p.splits = p.kps ? ceil_div(k, p.kps) : 1;  // splits that would be empty are dropped; K = 0: one, empty
   p.mtiles = ceil_div(m, (uint32_t)v.bm());
   p.stripes = ceil_div(n, (uint32_t)v.bn());
   p.grid = p.mtiles * p.stripes * p.splits;
@@ -251,6 +251,9 @@ Plan plan_stream(uint32_t m, uint32_t n, uint32_t k, uint64_t max_ws) {
 }
 
 Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws) {
+  // decide's contract admits N = 0 (nothing to launch: an empty grid) and K = 0 (the tiles run no
+  // stage and store the empty sum).
+  if (n == 0 || k == 0) return plan_make(0, 1, m, n, k, epi);
   if (m <= kStreamMaxM && n <= kStreamMaxN && k % 128 == 0 && n % 32 == 0) return plan_stream(m, n, k, max_ws);
   const Measured* near = nullptr;
   double best_rel = 0.12;

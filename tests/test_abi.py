@@ -160,6 +160,18 @@ def test_planner_invariants_on_random_shapes():
         assert p["ws_bytes"] <= 512 << 20, name
 
 
+@pytest.mark.parametrize("m", [1, 4, 603, 2307])
+def test_planner_handles_empty_n_and_k(m):
+    """decide's contract admits N = 0 and K = 0 (gemm.rs:140-144): N = 0 plans no workgroup at all, K = 0
+    one split of no stages whose tiles store the empty sum (zeros, or the residual unchanged)."""
+    for epi in Epilogue:
+        p = plan_for(m, 0, 128, epi)
+        assert p["workgroups"] == 0 and p["ws_bytes"] == 0, p
+        p = plan_for(m, 64, 0, epi)
+        assert p["splits"] == 1 and p["ws_bytes"] == 0 and p["workgroups"] == -(-m // p["bm"]), p
+    rc, err = bad_gemm(n=0)
+    assert rc == _lib.DH_EINVAL and "null context" in err  # the contract itself accepts N = 0
+
 def test_layout_functions_match_oracle():
     import oracle_lib as orc
 

@@ -172,6 +172,26 @@ def test_every_variant_stores_the_same_bits(gpu, kernels, stream):
         kernels.gemm.force(None)
 
 
+@pytest.mark.parametrize("m", [3, 203])
+def test_empty_k_and_n(gpu, kernels, stream, m):
+    """K = 0 stores the empty sum (zeros; AddF32 leaves the residual as it was); N = 0 launches nothing.
+    decide's contract admits both (gemm.rs:140-144)."""
+    x, w = to_dev(np.ones((m, 64), np.float16)), to_dev(np.ones((64, 64), np.float16))
+    y0 = synth.normal_f32(synth.seed_for(71), (m, 64), 1.0)
+    for epi in Epilogue:
+        out_cols = 32 if epi == Epilogue.SwigluF16 else 64
+        dt = np.float32 if epi in (Epilogue.StoreF32, Epilogue.AddF32) else np.float16
+        start = y0.astype(dt)[:, :out_cols].copy()
+        y = to_dev(start)
+        kernels.gemm.gemm(stream, (x, 0), (w, 0), (y, 0), m, 64, 0, 64, 64, out_cols, epi)
+        sync()
+        want = start if epi == Epilogue.AddF32 else np.zeros_like(start)
+        assert np.array_equal(to_host(y).view(np.uint8), want.view(np.uint8)), f"K = 0 {epi.name}"
+        y = to_dev(start)
+        kernels.gemm.gemm(stream, (x, 0), (w, 0), (y, 0), m, 0, 64, 64, 64, out_cols, epi)
+        sync()
+        assert np.array_equal(to_host(y).view(np.uint8), start.view(np.uint8)), f"N = 0 {epi.name}"
+
 def test_reference_kernel_matches_oracle(gpu, kernels_ref, stream):
     for (m, n, k) in [(5, 64, 96), (33, 96, 160), (70, 128, 2560)]:
         x, w = inputs(m, n, k, 400 + m)
