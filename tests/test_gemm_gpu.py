@@ -451,3 +451,35 @@ def test_random_shapes_planner_and_forced(gpu, kernels, stream, case):
             assert np.array_equal(got[:, out_cols:].view(np.uint8), y0[:, out_cols:].view(np.uint8)), label
     finally:
         kernels.gemm.force(None)
+
+
+@pytest.mark.parametrize("variant", range(len(variants())))
+def test_grouped_ragged_members_every_variant(gpu, kernels, stream, variant):
+    """One grouped launch per tile variant over members of mixed epilogues and widths that end mid-stripe
+    (96, 32 and 160 columns), K = 224 (three 64-wide stages and a 32-wide half stage), M = 41: every member
+    against the oracle, and the columns past each member's output untouched."""
+    m, k = 41, 224
+    specs = [(96, Epilogue.StoreF32), (32, Epilogue.AddF32), (160, Epilogue.SwigluF16)]
+    x = synth.normal_f16(synth.seed_for(81), (m, k), 1.0)
+    ws = [synth.normal_f16(synth.seed_for(82 + i), (n, k), 0.02) for i, (n, _) in enumerate(specs)]
+    ys, starts = [], []
+    for i, (n, epi) in enumerate(specs):
+        cols = n // 2 if epi == Epilogue.SwigluF16 else n
+        dt = np.float16 if epi == Epilogue.SwigluF16 else np.float32
+        start = synth.normal_f32(synth.seed_for(90 + i), (m, cols + 8), 1.0).astype(dt)
+        starts.append(start)
+        ys.append(to_dev(start))
+    members = [((to_dev(w), 0), k, n, (y, 0), s.shape[1], epi) for w, (n, epi), y, s in zip(ws, specs, ys, starts)]
+    try:
+        kernels.gemm.force(variant, 1)
+        kernels.gemm.gemm_grouped(stream, (to_dev(x), 0), k, m, k, members)
+        sync()
+    finally:
+        kernels.gemm.force(None)
+    for i, ((n, epi), w, y, start) in enumerate(zip(specs, ws, ys, starts)):
+        got = to_host(y)
+        cols = n // 2 if epi == Epilogue.SwigluF16 else n
+        y0 = start[:, :n].astype(np.float32) if epi == Epilogue.AddF32 else None
+        want = oracle_epi(x, w, epi, y0)
+        check_gemm(f"variant {variant} member {i} {epi.name}", got[:, :cols].astype(np.float32), want)
+        assert np.array_equal(got[:, cols:].view(np.uint8), start[:, cols:].view(np.uint8)), f"member {i} padding"
