@@ -1,0 +1,49 @@
+#!/usr/bin/env python3
+"""The path's GEMM shapes through the vendor library, for comparison only (not part of the product path).
+
+`torch.matmul` on ROCm dispatches fp16 GEMMs to hipBLASLt. This times Y = X·Wᵀ (plain store epilogue: no
+SwiGLU, no residual add) for the shapes decide_amd.shape_report measures with this build's kernels, with
+HIP events over 100 launches after 20 warm-ups. The kernel each shape runs, and its own duration, come from
+running this module under the profiler:
+
+    rocprofv3 --kernel-trace --stats -d gpurun_out/blas -o mm --output-format csv -- python3 -m decide_amd.vendor_report
+"""
+
+from __future__ import annotations
+
+import json
+
+SHAPES = [  # (name, M, N, K) — BASELINE's C1, the C2 MLP pair and the C4 gate|up
+    ("C1 proj", 276, 9216, 2560),
+    ("C2 gate|up", 603, 18432, 2560),
+    ("C2 down", 603, 2560, 9216),
+    ("C4 gate|up", 2307, 18432, 2560),
+]
+
+
+def main() -> None:
+    import torch
+
+    if not torch.cuda.is_available():
+        raise SystemExit("no GPU")
+    torch.manual_seed(0)
+    for name, m, n, k in SHAPES:
+        x = torch.randn(m, k, device="cuda", dtype=torch.float16)
+        w = torch.randn(n, k, device="cuda", dtype=torch.float16) * 0.02
+        for _ in range(20):
+            y = x @ w.t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(100):
+            y = x @ w.t()
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) / 100 * 1e3
+        print(json.dumps({"shape": name, "m": m, "n": n, "k": k, "event_us": round(us, 2),
+                          "tflops": round(2.0 * m * n * k / us / 1e6, 1)}), flush=True)
+        del y
+
+
+if __name__ == "__main__":
+    main()
