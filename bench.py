@@ -14,8 +14,10 @@ Prints ONE JSON line. `value` = the block's algorithmic TFLOP/s
 (2·M·N·K summed over both GEMMs ÷ time per step). `roofline` describes the
 dominant kernel (gate|up): its algorithmic TFLOP ÷ its average launch time,
 timed with HIP events on the stream it runs on, against 2.5 PFLOP/s dense
-fp16 MFMA. `cpu_baseline` times the oracle (decide's cpu_ref::gemm_nt
-restated in C: f64 sums, single thread) on a bounded sample of rows.
+fp16 MFMA. `cpu_baseline` times the whole block on the host's cores with the
+oracle's blocked fp32 GEMM, and beside it decide's cpu_ref::gemm_nt restated in
+C (f64 sums, single thread) on a bounded sample of rows. The config-5 forward
+(36 layers at 2,307 and 603 tokens) is timed first; see forward_timing.
 """
 
 from __future__ import annotations
@@ -69,15 +71,29 @@ def traffic_from_profile():
 
 
 def cpu_baseline(seconds: float):
-    """The oracle's faithful restatement of cpu_ref::gemm_nt (single-threaded, f64 sums) over a
-    bounded sample of the C2 block's rows, reported in TFLOP/s like the GPU value."""
+    """The C2 block on the host's CPU cores, in TFLOP/s like the GPU value (a reported baseline only):
+    (1) all cores: the blocked fp32 GEMM (oracle orc_gemm_f32_fast, OpenMP) over the whole block (all 603 rows),
+        median of 3 runs — the `value`;
+    (2) one core: the oracle's faithful restatement of decide's cpu_ref::gemm_nt (f64 sums,
+        cpu_ref.rs:24-35) over a bounded sample of rows (about `seconds` of CPU work)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as orc
     from decide_amd import synth
 
+    host_cores = len(os.sched_getaffinity(0))
+    threads = min(host_cores, 16)  # at most the GPU box's CPU share
     x = synth.normal_f16(synth.seed_for(21), (M, D), 1.0).astype(np.float32)
     wgu = synth.normal_f16(synth.seed_for(22), (2 * F, D), 0.02).astype(np.float32)
     wdn = synth.normal_f16(synth.seed_for(23), (D, F), 0.02).astype(np.float32)
+    block_flops = flops(M, 2 * F, D) + flops(M, D, F)
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        h = orc.f16_round(orc.swiglu_interleaved(orc.gemm_f32_fast(x, wgu, threads)))
+        orc.gemm_f32_fast(h, wdn, threads)
+        runs.append(time.perf_counter() - t0)
+    fast_s = float(np.median(runs))
+
     rows_done, elapsed, chunk = 0, 0.0, 8
     while rows_done < M and (elapsed < seconds or rows_done == 0):
         xs = x[rows_done:rows_done + chunk]
@@ -89,12 +105,20 @@ def cpu_baseline(seconds: float):
         rows_done += len(xs)
     work = flops(rows_done, 2 * F, D) + flops(rows_done, D, F)
     return {
-        "value": work / elapsed / 1e12,
+        "value": block_flops / fast_s / 1e12,
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{rows_done} of {M} rows of the C2 MLP block (gate|up + SwiGLU + down), "
-                  f"oracle cpu_ref::gemm_nt restatement, f64 sums, 1 thread, {elapsed:.1f} s",
+        "sample": f"the whole C2 block ({M} rows: gate|up + SwiGLU + down) with the oracle's blocked fp32 GEMM "
+                  f"(orc_gemm_f32_fast) on {threads} threads, median of 3 runs of {fast_s:.2f} s",
+        "host_cores": host_cores,
+        "faithful_single_thread": {
+            "value": work / elapsed / 1e12,
+            "unit": "TFLOP/s",
+            "cores": 1,
+            "sample": f"{rows_done} of {M} rows of the C2 block, oracle cpu_ref::gemm_nt restatement (f64 sums), "
+                      f"{elapsed:.1f} s",
+        },
     }
 
 
@@ -178,6 +202,9 @@ def main():
         print(json.dumps({"error": "no GPU"}))
         sys.exit(1)
     k = Kernels()
+    # The config-5 forward runs first: it is a workload of its own in this line, and its seconds of sustained
+    # MFMA load also leave the GPU at the clock it holds under load before the C2 block is timed.
+    fwd = None if args.no_forward else forward_timing(k, args.forward_runs)
     st = Stream()
     stream = st.handle
 
@@ -281,8 +308,8 @@ def main():
         },
         "wall_ms_timed_region": round(wall_ms, 2),
     }
-    if not args.no_forward:
-        out["forward"] = forward_timing(k, args.forward_runs)
+    if fwd is not None:
+        out["forward"] = fwd
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:

@@ -6,7 +6,7 @@ SwiGLU, no residual add) for the shapes decide_amd.shape_report measures with th
 HIP events over 100 launches after 20 warm-ups. The kernel each shape runs, and its own duration, come from
 running this module under the profiler:
 
-    rocprofv3 --kernel-trace --stats -d gpurun_out/blas -o mm --output-format csv -- python3 -m decide_amd.vendor_report
+    rocprofv3 --kernel-trace --stats -d gpurun_out/blas -o mm --output-format csv -- python3 bench_vendor.py
 """
 
 from __future__ import annotations

@@ -88,6 +88,7 @@ PROTOTYPES = {
         [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(DhGemmMember), c_uint32],
     ),
     "dh_gemm_plan_for": (c_int, [c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, POINTER(DhGemmPlan)]),
+    "dh_gemm_ws_need": (c_int, [c_void_p, c_uint32, c_uint32, c_uint32, POINTER(c_uint64)]),
     "dh_gemm_force": (c_int, [c_void_p, c_uint32, c_uint32]),
     "dh_gemm_variant_count": (c_uint32, []),
     "dh_gemm_variant_info": (

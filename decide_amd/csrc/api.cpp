@@ -50,23 +50,30 @@ void mark(dh_ctx* c, int kid) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-int ensure_aux(dh_ctx* c, uint64_t bytes) {
+namespace {
+// Grows *buf to at least `bytes` (by at least half its size, so a run of small
+// growths retires little); the old buffer joins c->retired.
+int grow(dh_ctx* c, float** buf, uint64_t* have, uint64_t bytes, uint64_t cap, const char* what) {
   std::lock_guard<std::mutex> g(c->ws_lock);
-  if (bytes <= c->aux_bytes) return DH_OK;
-  if (c->aux) {
-    hipError_t e = hipFree(c->aux);
-    c->aux = nullptr;
-    c->aux_bytes = 0;
-    if (e != hipSuccess) return fail(DH_EDEVICE, "forward workspace: hipFree: %s", hipGetErrorString(e));
-  }
+  if (bytes <= *have) return DH_OK;
+  if (bytes > cap)
+    return fail(DH_ENOMEM, "%s of %llu bytes exceeds its %llu-byte ceiling", what, (unsigned long long)bytes,
+                (unsigned long long)cap);
+  const uint64_t want = std::min(cap, std::max(bytes, *have + *have / 2));
   void* p = nullptr;
-  hipError_t e = hipMalloc(&p, bytes);
+  hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess)
-    return fail(DH_ENOMEM, "forward workspace of %llu bytes: %s", (unsigned long long)bytes, hipGetErrorString(e));
-  c->aux = (float*)p;
-  c->aux_bytes = bytes;
+    return fail(DH_ENOMEM, "%s of %llu bytes: %s", what, (unsigned long long)want, hipGetErrorString(e));
+  if (*buf) c->retired.push_back(*buf);
+  *buf = (float*)p;
+  *have = want;
   return DH_OK;
 }
+}  // namespace
+
+int ensure_aux(dh_ctx* c, uint64_t bytes) { return grow(c, &c->aux, &c->aux_bytes, bytes, UINT64_MAX, "forward workspace"); }
+
+int ensure_ws(dh_ctx* c, uint64_t bytes) { return grow(c, &c->ws, &c->ws_bytes, bytes, c->ws_cap, "split-K workspace"); }
 
 }  // namespace dh_api
 
@@ -74,9 +81,9 @@ using namespace dh_api;
 
 namespace {
 
-// gemm.rs:140-144 and 159-163.
-int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const void* y, uint32_t ldy, uint32_t m,
-               uint32_t n, uint32_t k, uint32_t epi) {
+// gemm.rs:140-144: what every implementation asserts.
+int check_gemm_common(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const void* y, uint32_t ldy,
+                      uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
   if (epi > 3u) return fail(DH_EINVAL, "gemm: epilogue %u is not one of 0..3", epi);
   if (n % 32 != 0 || k % 32 != 0)
     return fail(DH_EINVAL, "gemm: N = %u and K = %u must be multiples of 32", n, k);
@@ -85,6 +92,15 @@ int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const v
     return fail(DH_EINVAL, "gemm: row strides ldx = %u, ldw = %u must cover K = %u", ldx, ldw, k);
   const uint32_t y_cols = epi == DH_EPI_SWIGLU_F16 ? n / 2 : n;
   if (ldy < y_cols) return fail(DH_EINVAL, "gemm: row stride ldy = %u must cover the %u output columns", ldy, y_cols);
+  if (!x || !w || !y) return fail(DH_EINVAL, "gemm: null operand");
+  return DH_OK;
+}
+
+// gemm.rs:159-163: the fast kernels' extra requirements (decide's baseline
+// returns before these asserts, gemm.rs:150-156), plus this build's 4 GiB
+// row-span limit of the tile kernel's DMA offsets.
+int check_gemm_fast(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const void* y, uint32_t ldy,
+                    uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
   if (ldx % 8 != 0 || ldw % 8 != 0)
     return fail(DH_EINVAL, "gemm (fast): ldx = %u and ldw = %u must be multiples of 8", ldx, ldw);
   if (!aligned(x, 16) || !aligned(w, 16))
@@ -92,7 +108,6 @@ int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const v
   if (ldy % 2 != 0) return fail(DH_EINVAL, "gemm (fast): ldy = %u must be even", ldy);
   const uintptr_t y_align = (epi == DH_EPI_STORE_F32 || epi == DH_EPI_ADD_F32) ? 8 : 4;
   if (!aligned(y, y_align)) return fail(DH_EINVAL, "gemm (fast): y address %p must be a multiple of %u", y, (unsigned)y_align);
-  if (!x || !w || !y) return fail(DH_EINVAL, "gemm: null operand");
   // The tile kernel's DMA addresses a row as a 32-bit byte offset from the operand's base.
   if ((uint64_t)(m - 1) * ldx * 2 + (uint64_t)k * 2 > UINT32_MAX)
     return fail(DH_EINVAL, "gemm: X rows span more than 4 GiB (m = %u, ldx = %u); split the call along M", m, ldx);
@@ -101,22 +116,21 @@ int check_gemm(const void* x, uint32_t ldx, const void* w, uint32_t ldw, const v
   return DH_OK;
 }
 
-int ensure_ws(dh_ctx* c, uint64_t bytes) {
-  std::lock_guard<std::mutex> g(c->ws_lock);
-  if (bytes <= c->ws_bytes) return DH_OK;
-  if (c->ws) {
-    hipError_t e = hipFree(c->ws);
-    c->ws = nullptr;
-    c->ws_bytes = 0;
-    if (e != hipSuccess) return fail(DH_EDEVICE, "split-K workspace: hipFree: %s", hipGetErrorString(e));
-  }
-  void* p = nullptr;
-  hipError_t e = hipMalloc(&p, bytes);
-  if (e != hipSuccess) return fail(DH_ENOMEM, "split-K workspace of %llu bytes: %s", (unsigned long long)bytes,
-                                   hipGetErrorString(e));
-  c->ws = (float*)p;
-  c->ws_bytes = bytes;
+// The reference kernel reads and writes single elements: only their natural alignment is needed.
+int check_gemm_reference(const void* x, const void* w, const void* y, uint32_t epi) {
+  const uintptr_t y_align = (epi == DH_EPI_STORE_F32 || epi == DH_EPI_ADD_F32) ? 4 : 2;
+  if (!aligned(x, 2) || !aligned(w, 2) || !aligned(y, y_align))
+    return fail(DH_EINVAL, "gemm (reference): x/w/y addresses %p/%p/%p must be aligned to their element sizes", x,
+                w, y);
   return DH_OK;
+}
+
+int check_gemm(const dh_ctx* c, const void* x, uint32_t ldx, const void* w, uint32_t ldw, const void* y,
+               uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
+  int rc = check_gemm_common(x, ldx, w, ldw, y, ldy, m, n, k, epi);
+  if (rc != DH_OK) return rc;
+  if (c && (c->flags & DH_GEMM_REFERENCE)) return check_gemm_reference(x, w, y, epi);
+  return check_gemm_fast(x, ldx, w, ldw, y, ldy, m, n, k, epi);
 }
 
 dh::Plan choose_plan(const dh_ctx* c, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
@@ -211,6 +225,7 @@ void dh_ctx_destroy(dh_ctx* ctx) {
   if (!ctx) return;
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->aux) (void)hipFree(ctx->aux);
+  for (void* p : ctx->retired) (void)hipFree(p);
   delete ctx;
 }
 
@@ -220,7 +235,7 @@ uint32_t dh_variants_loaded(const dh_ctx* ctx) {
 
 int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
                uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
-  int rc = check_gemm(x, ldx, w, ldw, y, ldy, m, n, k, epi);
+  int rc = check_gemm(ctx, x, ldx, w, ldw, y, ldy, m, n, k, epi);
   if (rc != DH_OK) return rc;
   if (!ctx) return fail(DH_EINVAL, "gemm: null context");
   hipStream_t s = (hipStream_t)stream;
@@ -245,7 +260,7 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
   for (uint32_t i = 0; i < count; ++i) {
     const dh_gemm_member& mb = members[i];
     ns[i] = mb.n;
-    int rc = check_gemm(x, ldx, mb.w, mb.ldw, mb.y, mb.ldy, m, mb.n, k, mb.epi);
+    int rc = check_gemm(ctx, x, ldx, mb.w, mb.ldw, mb.y, mb.ldy, m, mb.n, k, mb.epi);
     if (rc != DH_OK) {
       std::string msg = g_err;
       return fail(rc, "member %u: %s", i, msg.c_str());
@@ -295,6 +310,13 @@ int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint
   return ok();
 }
 
+int dh_gemm_ws_need(const dh_ctx* ctx, uint32_t max_m, uint32_t n, uint32_t k, uint64_t* out) {
+  if (!out) return fail(DH_EINVAL, "dh_gemm_ws_need: out is NULL");
+  if (max_m < 1 || n % 32 || k % 32) return fail(DH_EINVAL, "dh_gemm_ws_need: invalid shape");
+  *out = dh::plan_ws_need(max_m, n, k, ctx ? ctx->ws_cap : (512ull << 20));
+  return ok();
+}
+
 int dh_gemm_force(dh_ctx* ctx, uint32_t variant, uint32_t splits) {
   if (!ctx) return fail(DH_EINVAL, "dh_gemm_force: null context");
   if (variant == UINT32_MAX) {
@@ -326,19 +348,12 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
   if (!ctx) return fail(DH_EINVAL, "dh_warm_up: null context");
   hipStream_t s = (hipStream_t)stream;
   // Size the workspace for the largest split-K plan of decide's engine shapes
-  // (gemm_configs.rs:385) at max_m rows.
+  // (gemm_configs.rs:385) at any M up to max_m rows, so no such call grows it.
   static const uint32_t kShapes[][2] = {{2560, 12352}, {2560, 10240}, {2560, 18432}, {4096, 2560},
                                         {9216, 2560},  {2560, 2048},  {2560, 8192},  {2560, 6144}};
   uint64_t need = 0;
-  for (auto& kn : kShapes)
-    for (uint32_t epi = 0; epi < 4; ++epi) {
-      for (uint32_t m = 1; m <= std::max(1u, max_m); m = m < 16 ? m + 1 : m * 2) {
-        const dh::Plan p = choose_plan(ctx, m, kn[1], kn[0], epi);
-        need = std::max(need, p.ws_bytes);
-      }
-      const dh::Plan p = choose_plan(ctx, std::max(1u, max_m), kn[1], kn[0], epi);
-      need = std::max(need, p.ws_bytes);
-    }
+  if (ctx->forced_variant < 0 && !(ctx->flags & DH_GEMM_REFERENCE))
+    for (auto& kn : kShapes) need = std::max(need, dh::plan_ws_need(std::max(1u, max_m), kn[1], kn[0], ctx->ws_cap));
   if (need) {
     int rc = ensure_ws(ctx, need);
     if (rc != DH_OK) return rc;

@@ -7,6 +7,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "../../include/decide_hip.h"
 
@@ -19,6 +20,9 @@ struct dh_ctx {
   uint64_t ws_cap = 512ull << 20;  // split-K workspace ceiling
   float* aux = nullptr;            // forward-kernel workspace (the chunked recurrence's per-chunk matrices)
   uint64_t aux_bytes = 0;
+  // Workspaces a growth replaced. A captured graph holds the raw pointers it was
+  // captured with, so superseded buffers stay allocated until dh_ctx_destroy.
+  std::vector<void*> retired;
   int forced_variant = -1;
   uint32_t forced_splits = 0;
   std::atomic<uint64_t> used{0};  // bit per distinct kernel launched
@@ -45,7 +49,10 @@ int hip_status(hipError_t e, const char* what);
 // Records that kernel `kid` has been launched through this context.
 void mark(dh_ctx* c, int kid);
 bool aligned(const void* p, uintptr_t a);
-// Grows the context's forward-kernel workspace to at least `bytes` (hipMalloc only when it grows).
+// Grows the context's forward-kernel workspace to at least `bytes` (hipMalloc only when it grows; the
+// old buffer is retired, not freed).
 int ensure_aux(dh_ctx* c, uint64_t bytes);
+// The same for the split-K workspace, never beyond c->ws_cap.
+int ensure_ws(dh_ctx* c, uint64_t bytes);
 
 }  // namespace dh_api

@@ -272,6 +272,13 @@ Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws
   return plan_model(m, n, k, epi, max_ws);
 }
 
+uint64_t plan_ws_need(uint32_t max_m, uint32_t n, uint32_t k, uint64_t max_ws) {
+  uint64_t need = 0;
+  for (uint32_t m = 1; m <= max_m; ++m)
+    for (uint32_t epi = 0; epi < 4; ++epi) need = std::max(need, plan_gemm(m, n, k, epi, max_ws).ws_bytes);
+  return need;
+}
+
 Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count) {
   // Members share X and launch together: plan as one GEMM of the summed width
   // (the table's row for that width is measured on the grouped launch where

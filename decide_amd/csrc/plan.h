@@ -39,6 +39,11 @@ Plan plan_make(int variant, uint32_t splits, uint32_t m, uint32_t n, uint32_t k,
 Plan plan_stream(uint32_t m, uint32_t n, uint32_t k, uint64_t max_ws);
 // Best plan for a single GEMM. `max_ws` caps the split-K workspace bytes.
 Plan plan_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t epi, uint64_t max_ws);
+// The largest split-K workspace plan_gemm asks for over every M in 1..max_m and
+// every epilogue at (n, k): the workspace a caller must hold so that no call of
+// up to max_m rows grows it. The table switches split counts between measured
+// rows, so the need is not monotone in M; this sweeps every M.
+uint64_t plan_ws_need(uint32_t max_m, uint32_t n, uint32_t k, uint64_t max_ws);
 // Best plan for a grouped launch of `count` members of widths ns[] that share
 // X (no split-K). Each member rounds up to whole column stripes of its own.
 Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count);

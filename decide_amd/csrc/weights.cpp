@@ -17,6 +17,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -235,7 +236,12 @@ int dh_model_load(dh_model* model, const char* dir) {
     const Json* jd = e->get("dtype");
     const Json* js = e->get("shape");
     if (!jb || jb->kind != Json::Str) return fail(DH_EINVAL, "tensor %s: missing or bad blob", name);
-    if (!jo || jo->kind != Json::Num || jo->num < 0) return fail(DH_EINVAL, "tensor %s: missing or bad offset", name);
+    // Offsets and dims are JSON numbers (doubles): only integral values up to 2^53 convert to u64 exactly
+    // (decide reads them with as_u64, weights.rs:160-171).
+    auto exact_u64 = [](const Json* j) {
+      return j && j->kind == Json::Num && j->num >= 0 && j->num <= 9007199254740992.0 && std::floor(j->num) == j->num;
+    };
+    if (!exact_u64(jo)) return fail(DH_EINVAL, "tensor %s: missing or bad offset", name);
     if (!jd || jd->kind != Json::Str) return fail(DH_EINVAL, "tensor %s: missing or bad dtype", name);
     if (!js || js->kind != Json::Arr) return fail(DH_EINVAL, "tensor %s: missing or bad shape", name);
     bool known = false;
@@ -244,8 +250,9 @@ int dh_model_load(dh_model* model, const char* dir) {
     if (code != dtype) return fail(DH_EINVAL, "tensor %s is %s; the model holds it as dtype %u", name, jd->str.c_str(), dtype);
     uint64_t n = 1;
     for (const Json& d : js->arr) {
-      if (d.kind != Json::Num || d.num < 0) return fail(DH_EINVAL, "tensor %s: missing or bad shape", name);
-      n *= (uint64_t)d.num;
+      if (!exact_u64(&d)) return fail(DH_EINVAL, "tensor %s: missing or bad shape", name);
+      if (__builtin_mul_overflow(n, (uint64_t)d.num, &n))
+        return fail(DH_EINVAL, "tensor %s: shape element count overflows", name);
     }
     if (n != elems) return fail(DH_EINVAL, "tensor %s has %llu elements; the model expects %llu", name,
                                 (unsigned long long)n, (unsigned long long)elems);
@@ -256,7 +263,7 @@ int dh_model_load(dh_model* model, const char* dir) {
     if (it == maps.end())
       return fail(DH_EINVAL, "tensor %s is in %s, which is not in the blob list", name, jb->str.c_str());
     const uint64_t bytes = elems * (dtype == 2 ? 4 : 2);
-    if (off + bytes > it->second->len) return fail(DH_EINVAL, "tensor %s runs past the end of %s", name, jb->str.c_str());
+    if (off > it->second->len || bytes > it->second->len - off) return fail(DH_EINVAL, "tensor %s runs past the end of %s", name, jb->str.c_str());
     const hipError_t err = hipMemcpy(dst, (const char*)it->second->ptr + off, bytes, hipMemcpyHostToDevice);
     if (err != hipSuccess) return fail(DH_EDEVICE, "model_load: copying %s: %s", name, hipGetErrorString(err));
   }

@@ -13,10 +13,15 @@
  *     calling thread's dh_last_error() holds a one-line message. Contract
  *     violations are reported before anything is launched.
  * The library never allocates or frees caller memory. A context owns only its
- * launch plan and a split-K workspace (device memory it allocates itself).
- * A context is immutable after dh_ctx_create apart from that workspace, which
- * grows under an internal lock; launches on different streams that share a
- * context must not run split-K GEMMs concurrently (they share the workspace).
+ * launch plan and two workspaces (device memory it allocates itself): the
+ * split-K partials and the forward kernels' scratch. A context is immutable
+ * after dh_ctx_create apart from those workspaces, which grow under an
+ * internal lock; launches on different streams that share a context must not
+ * run split-K GEMMs concurrently (they share the workspace). A workspace that
+ * grows is replaced, and the buffer it replaces stays allocated until
+ * dh_ctx_destroy, so a graph captured earlier (dh_model_capture) never reads
+ * freed memory; it keeps reading the buffers it was captured with, so replays
+ * of one graph must not overlap work that uses those buffers.
  */
 #ifndef DECIDE_HIP_H
 #define DECIDE_HIP_H
@@ -103,7 +108,9 @@ uint32_t dh_variants_loaded(const dh_ctx* ctx);
  * 8-byte (fp32 outputs) or 4-byte (fp16 outputs) aligned, and X's and W's rows
  * each within 4 GiB of their base: ((m - 1)·ldx + k)·2 and ((n - 1)·ldw + k)·2
  * at most 2^32 - 1 bytes (no such limit in decide; its engine shapes are far
- * below it). */
+ * below it). A DH_GEMM_REFERENCE context checks only the first part, as
+ * decide's baseline does (gemm.rs:140-156): shapes and strides, plus each
+ * operand aligned to its own element size. */
 int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
                uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
 
@@ -118,6 +125,11 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
 /* The plan dh_gemm_nt would use (no launch, no device needed; decide:
  * gemm_configs::plan, crates/decide-metal/src/gemm_configs.rs:311-314). */
 int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint32_t epi, dh_gemm_plan* out);
+/* The split-K workspace (bytes) that dh_gemm_nt's planner asks for at its
+ * largest over every m in 1..max_m and every epilogue at (n, k), on this
+ * context (no device needed). dh_warm_up holds at least this for decide's
+ * engine shapes; a caller with other shapes can size its own calls with it. */
+int dh_gemm_ws_need(const dh_ctx* ctx, uint32_t max_m, uint32_t n, uint32_t k, uint64_t* out);
 /* Forces the next GEMMs on this context to use `variant` and `splits`
  * (variant = UINT32_MAX restores the planner). For tuning sweeps only. */
 int dh_gemm_force(dh_ctx* ctx, uint32_t variant, uint32_t splits);

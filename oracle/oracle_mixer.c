@@ -97,8 +97,10 @@ void orc_conv_state_update(const float* p, uint32_t ldp, uint32_t t, const float
  * place; a, b rows of stride ldab (value head h at column h); o [t][NV][DV]. */
 void orc_gated_delta(const float* q, const float* k, const float* v, const float* a, const float* b, uint32_t ldab,
                      const float* a_log, const float* dt_bias, float* state, uint32_t t, float* o) {
-  for (uint32_t s = 0; s < t; ++s) {
-    for (int h = 0; h < NV; ++h) {
+  /* value heads never interact: each runs its own steps (threads split the heads; same arithmetic) */
+#pragma omp parallel for schedule(static)
+  for (int h = 0; h < NV; ++h) {
+    for (uint32_t s = 0; s < t; ++s) {
       const int hk = h / (NV / NK);
       const float g = expf(-(expf(a_log[h])) * softplus(a[(size_t)s * ldab + h] + dt_bias[h]));
       const float beta = sigmoid(b[(size_t)s * ldab + h]);

@@ -207,3 +207,71 @@ def test_bf16_to_f16_rne_and_overflow_gate():
     o = np.empty_like(big)
     assert lib.dh_bf16_to_f16(big.ctypes.data, o.ctypes.data, 1, counts) == _lib.DH_EINVAL
     assert counts[3] == 1
+
+
+def _split_args(text):
+    """Top-level comma-separated arguments of one parameter list."""
+    args, depth, cur = [], 0, ""
+    for ch in text:
+        if ch in "([<":
+            depth += 1
+        elif ch in ")]>":
+            depth -= 1
+        if ch == "," and depth == 0:
+            args.append(cur)
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        args.append(cur)
+    return [a.strip() for a in args if a.strip() and a.strip() != "void"]
+
+
+def header_prototypes():
+    """{name: argument count} of every function include/decide_hip.h declares."""
+    with open(os.path.join(ROOT, "include", "decide_hip.h")) as f:
+        text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    protos = {}
+    for m in re.finditer(r"\b(dh_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        protos[m.group(1)] = len(_split_args(m.group(2)))
+    return protos
+
+
+def rust_prototypes():
+    """{name: argument count} of the `extern "C"` block INTEGRATION.md shows for the decide-hip crate."""
+    with open(os.path.join(ROOT, "INTEGRATION.md")) as f:
+        text = f.read()
+    start = text.index('extern "C" {')
+    body = text[start:text.index("\n}\n", start)]
+    protos = {}
+    for m in re.finditer(r"pub fn (dh_[a-z0-9_]+)\s*\((.*?)\)\s*(->[^;]*)?;", body, flags=re.S):
+        assert m.group(1) not in protos, f"{m.group(1)} is bound twice"
+        protos[m.group(1)] = len(_split_args(m.group(2)))
+    return protos
+
+
+def test_rust_binding_matches_the_header():
+    header, rust = header_prototypes(), rust_prototypes()
+    assert sorted(header) == declared_symbols()
+    assert sorted(rust) == sorted(header), (sorted(set(header) - set(rust)), sorted(set(rust) - set(header)))
+    for name, n in header.items():
+        assert rust[name] == n, f"{name}: {rust[name]} arguments in the Rust binding, {n} in the header"
+
+
+@pytest.mark.parametrize("kn", [(9216, 2560), (4096, 2560), (2560, 18432)])
+def test_workspace_need_covers_every_m(kn):
+    """dh_gemm_ws_need (what dh_warm_up holds) is the maximum of every plan's workspace for M in 1..max_m:
+    the planner's table switches split counts between measured rows, so the need is not monotone in M."""
+    k, n = kn
+    lib = _lib.load()
+    max_m = 1200
+    need = ctypes.c_uint64()
+    _lib.check(lib.dh_gemm_ws_need(None, max_m, n, k, ctypes.byref(need)))
+    brute = 0
+    for m in range(1, max_m + 1):
+        for epi in range(4):
+            brute = max(brute, plan_for(m, n, k, Epilogue(epi))["ws_bytes"])
+    assert need.value == brute
+    # the point of the sweep: a larger M can need less than a smaller one
+    if kn == (9216, 2560):
+        assert plan_for(1146, n, k, Epilogue.AddF32)["ws_bytes"] > plan_for(2307, n, k, Epilogue.AddF32)["ws_bytes"]

@@ -1,0 +1,174 @@
+"""BASELINE config 5 at the size its targets are stated on: the 4B-shaped hybrid forward (36 layers, every 4th
+full attention, d 2560, d_ff 9216) over a 2,307-token prompt, bar max |Δlogit| <= 0.01.
+
+The oracle forward (tests/oracle_forward.py: cpu_ref.rs pieces with decide's rounding points, forward.rs:1118-1310)
+runs at the two extremes the CPU can finish in about a minute each:
+  * depth: all 36 layers at T = 256, the last layer pruned to 3 answer rows;
+  * length: 4 layers at T = 2,307 (the chunked recurrence over 2,307 steps and 2,307-key causal attention over every
+    row, no pruning).
+The full shape itself (36 layers, T = 2,307, vocab 151,936, 3 answers x 8 candidates) is checked through properties
+that need no oracle: bitwise run-to-run determinism, graph replay equal to eager, pruned within 1e-3 of unpruned,
+agreement within 0.01 with an independent GPU implementation (the M-independent reference GEMM kernel and the
+token-by-token recurrence), and one closed form of the layer wiring: with every w_out and w_down zero the residual
+stream never leaves the embedding rows, so the logits are final_head of the answers' embedding rows."""
+
+import numpy as np
+import pytest
+
+import oracle_forward
+import oracle_lib as orc
+from decide_amd import synth
+from decide_amd.forward import Model, ModelConfig
+from decide_amd.hip import rt
+from decide_amd.kernels import GemmImpl, Kernels
+from gpu_util import full, sync, to_dev, to_host
+from test_forward_gpu import MAX_LOGIT_DIFF, _names, _shape
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, T_FULL, VOCAB, ANSWERS, CANDS = 36, 2307, 151936, 3, 8
+
+
+def _request(t, vocab, seed, answers=ANSWERS, cands=CANDS):
+    ids = synth.uniform_ids(synth.seed_for(seed), t, vocab).astype(np.uint32)
+    ans = np.array([t // 3, (2 * t) // 3, t - 1], np.uint32)[:answers]
+    cand = synth.uniform_ids(synth.seed_for(seed + 1), answers * cands, vocab).astype(np.uint32).reshape(answers,
+                                                                                                         cands)
+    ncand = np.full(answers, cands, np.uint32)
+    ncand[1] = cands - 2  # ragged
+    return ids, ans, cand, ncand
+
+
+def _forward(model, ids, ans, cand, ncand, prune=True):
+    logits = full((len(ans), model.cfg.max_cand), np.float32, np.nan)
+    model.forward(0, (to_dev(ids), 0), len(ids), (to_dev(ans), 0), len(ans), (to_dev(cand), 0), (to_dev(ncand), 0),
+                  (logits, 0), prune=prune)
+    sync()
+    return to_host(logits)
+
+
+def _weights(model, layers):
+    return {name: model.download(name).reshape(_shape(name, model.tensor(name)[1])) for name in _names(layers)}
+
+
+def _check_against_oracle(kernels, layers, t, prune, seed):
+    cfg = ModelConfig(layers=layers, vocab=4096, max_tokens=t, max_answers=ANSWERS, max_cand=CANDS)
+    model = Model(kernels.ctx, cfg)
+    kernels.gemm.warm_up(0, max_m=t)
+    model.init_random(0, seed=seed)
+    sync()
+    ids, ans, cand, ncand = _request(t, cfg.vocab, seed + 7)
+    got = _forward(model, ids, ans, cand, ncand, prune)
+    W = _weights(model, layers)
+    model.close()
+    want = oracle_forward.forward(W, layers, ids, ans, cand, ncand, cfg.max_cand, prune=prune)
+    written = ~np.isnan(want)
+    assert np.array_equal(~np.isnan(got), written), "entries past ncand must stay untouched"
+    assert np.isfinite(got[written]).all()
+    diff = np.abs(got[written] - want[written])
+    print(f"layers {layers} T {t}: max |Δlogit| {diff.max():.3g} over logits up to {np.abs(want[written]).max():.3g}")
+    assert diff.max() <= MAX_LOGIT_DIFF, f"max |Δlogit| {diff.max():.4g}"
+
+
+def test_forward_matches_oracle_at_depth(gpu, kernels):
+    """All 36 layers (27 Gated-DeltaNet, 9 gated attention; the last one pruned) at T = 256."""
+    _check_against_oracle(kernels, LAYERS, 256, True, seed=5100)
+
+
+def test_forward_matches_oracle_at_length(gpu, kernels):
+    """4 layers (three Gated-DeltaNet on the chunked recurrence, then full attention over all 2,307 rows)."""
+    _check_against_oracle(kernels, 4, T_FULL, False, seed=5200)
+
+
+@pytest.fixture(scope="module")
+def full_model(kernels):
+    cfg = ModelConfig(layers=LAYERS, vocab=VOCAB, max_tokens=T_FULL, max_answers=ANSWERS, max_cand=CANDS)
+    model = Model(kernels.ctx, cfg)
+    kernels.gemm.warm_up(0, max_m=T_FULL)
+    model.init_random(0, seed=0xDEC1DE)
+    sync()
+    yield model
+    model.close()
+
+
+@pytest.fixture(scope="module")
+def full_request():
+    return _request(T_FULL, VOCAB, 5300)
+
+
+def test_full_shape_is_finite_and_deterministic(gpu, full_model, full_request):
+    a = _forward(full_model, *full_request)
+    b = _forward(full_model, *full_request)
+    written = ~np.isnan(a)
+    assert written.sum() == ANSWERS * CANDS - 2
+    assert np.isfinite(a[written]).all()
+    np.testing.assert_array_equal(a, b)
+
+
+def test_full_shape_graph_replays_equal_eager(gpu, full_model, full_request):
+    from decide_amd.hip import Stream
+
+    ids, ans, cand, ncand = full_request
+    eager = _forward(full_model, ids, ans, cand, ncand)
+    st = Stream()
+    dev = [to_dev(a) for a in (ids, ans, cand, ncand)]
+    logits = full((ANSWERS, CANDS), np.float32, np.nan)
+    graph = full_model.capture(st.handle, (dev[0], 0), T_FULL, (dev[1], 0), ANSWERS, (dev[2], 0), (dev[3], 0),
+                               (logits, 0))
+    for i in range(3):
+        logits.copy_from(np.full((ANSWERS, CANDS), np.nan, np.float32))
+        graph.launch(st.handle)
+        st.synchronize()
+        np.testing.assert_array_equal(to_host(logits), eager, err_msg=f"replay {i}")
+        _forward(full_model, ids[:600], ans[:1] % 600, cand[:1], ncand[:1])  # eager work of another size between
+    graph.close()
+    st.destroy()
+
+
+def test_full_shape_pruned_equals_unpruned(gpu, full_model, full_request):
+    a = _forward(full_model, *full_request, prune=True)
+    b = _forward(full_model, *full_request, prune=False)
+    w = ~np.isnan(a)
+    assert np.array_equal(w, ~np.isnan(b))
+    assert np.abs(a[w] - b[w]).max() <= 1e-3
+
+
+def test_full_shape_agrees_with_the_reference_implementations(gpu, full_model, full_request):
+    """The fast path against a context whose GEMMs run the M-independent reference kernel (fp32 FMA over K in order)
+    and whose recurrence runs token by token, on the same random-init weights."""
+    fast = _forward(full_model, *full_request)
+    ref = Kernels(GemmImpl.Baseline, delta="sequential")
+    model = Model(ref.ctx, full_model.cfg)
+    model.init_random(0, seed=0xDEC1DE)
+    slow = _forward(model, *full_request)
+    model.close()
+    ref.ctx.close()
+    w = ~np.isnan(fast)
+    assert np.array_equal(w, ~np.isnan(slow))
+    diff = np.abs(fast[w] - slow[w]).max()
+    print(f"fast vs reference implementations: max |Δlogit| {diff:.3g}")
+    assert diff <= MAX_LOGIT_DIFF
+
+
+def test_zero_projections_leave_the_embedding(gpu, kernels, full_request):
+    """Closed form of the composition: every mixer and MLP output enters x only through w_out and w_down
+    (x += g·w_outᵀ, x += mlp·w_downᵀ; forward.rs:1256-1282), so with both zero the answer rows reach the head as
+    their embedding rows, and the logits are final_head(embed[ids[ans]]) (cpu_ref.rs:190-198)."""
+    cfg = ModelConfig(layers=LAYERS, vocab=VOCAB, max_tokens=T_FULL, max_answers=ANSWERS, max_cand=CANDS)
+    model = Model(kernels.ctx, cfg)
+    model.init_random(0, seed=0xC105ED)
+    for l in range(LAYERS):
+        for name in ("w_out", "w_down"):
+            ptr, n, dtype = model.tensor(f"L{l}.{name}")
+            assert rt().hipMemset(ptr, 0, n * np.dtype(dtype).itemsize) == 0
+    sync()
+    ids, ans, cand, ncand = full_request
+    got = _forward(model, ids, ans, cand, ncand)
+    table = model.download("embed").reshape(VOCAB, 2560)
+    x = orc.embed_bf16(ids[ans], table)
+    want = orc.final_head(x, model.download("final_norm"), table, cand, ncand, CANDS)
+    model.close()
+    w = ~np.isnan(want)
+    assert np.array_equal(w, ~np.isnan(got))
+    diff = np.abs(got[w] - want[w]).max()
+    assert diff <= 1e-4, f"max |Δlogit| {diff:.3g}"

@@ -1,8 +1,9 @@
 """The whole hybrid decoder forward on the GPU (dh_model_forward) against the oracle's forward built from
 cpu_ref.rs pieces with decide's rounding points, on a reduced random-init model (same layer shapes, fewer
 layers, small vocab and prompt). Bar: max |Δlogit| <= 0.01.
-The full-size forward (36 layers, 2,307 tokens) is measured by bench.py --forward; here it is checked
-through size-independent properties: finite logits and bitwise determinism across runs."""
+The forward at its stated size (36 layers, 2,307 tokens, vocab 151,936) is checked in test_forward_c5_gpu.py:
+against the oracle at full depth (T = 256) and at full length (4 layers, T = 2,307), and at the full shape
+through determinism, graph replay, pruning, an independent GPU implementation and a closed form."""
 
 import numpy as np
 import pytest
@@ -155,3 +156,38 @@ def test_forward_delta_implementations_agree(gpu, kernels, kernels_delta_sequent
     w = ~np.isnan(out[0])
     assert np.array_equal(w, ~np.isnan(out[1]))
     assert np.abs(out[0][w] - out[1][w]).max() <= MAX_LOGIT_DIFF
+
+
+def test_graph_survives_workspace_growth(gpu):
+    """A graph keeps the raw workspace pointers it was captured with. Capture at T = 603 (split-K down and out
+    projections), then run an eager forward at T = 1146 on a fresh context without warm-up, which grows the split-K
+    workspace: the replayed graph must still reproduce the eager T = 603 forward (the replaced workspace stays
+    allocated until the context is destroyed)."""
+    from decide_amd.hip import Stream
+    from decide_amd.kernels import Kernels
+
+    k = Kernels()
+    cfg = ModelConfig(layers=4, vocab=600, max_tokens=1146, max_answers=3, max_cand=5)
+    model = Model(k.ctx, cfg)
+    st = Stream()
+    s = st.handle
+    model.init_random(s, seed=95)
+    ids, ans, cand, ncand = _request(603, cfg.vocab, 3, cfg.max_cand, 450)
+    dev = [to_dev(a) for a in (ids, ans, cand, ncand)]
+    logits = full((3, cfg.max_cand), np.float32, np.nan)
+    graph = model.capture(s, (dev[0], 0), 603, (dev[1], 0), 3, (dev[2], 0), (dev[3], 0), (logits, 0))
+    st.synchronize()
+    eager = to_host(logits)
+    before = k.gemm.plan(1146, 2560, 9216, 2)["ws_bytes"]
+    long_ids, long_ans, long_cand, long_ncand = _request(1146, cfg.vocab, 3, cfg.max_cand, 451)
+    _run(model, k, long_ids, long_ans, long_cand, long_ncand, cfg.max_cand, True)
+    assert before > k.gemm.plan(603, 2560, 9216, 2)["ws_bytes"], "the T = 1146 forward must need a larger workspace"
+    for i in range(2):
+        logits.copy_from(np.full((3, cfg.max_cand), np.nan, np.float32))
+        graph.launch(s)
+        st.synchronize()
+        np.testing.assert_array_equal(to_host(logits), eager, err_msg=f"replay {i}")
+    graph.close()
+    st.destroy()
+    model.close()
+    k.ctx.close()

@@ -201,6 +201,39 @@ def test_reference_kernel_matches_oracle(gpu, kernels_ref, stream):
             check_gemm(f"reference m{m} {epi.name}", got, oracle_epi(x, w, epi, y0))
 
 
+def test_reference_kernel_takes_what_decides_baseline_takes(gpu, kernels, kernels_ref, stream):
+    """decide's baseline returns before the fast path's alignment asserts (gemm.rs:150-163): strides that are not
+    multiples of 8, x/w at 2-byte offsets and y at element offsets are accepted there and computed correctly;
+    the fast context still refuses them."""
+    m, n, k = 21, 64, 96
+    ldx, ldw = k + 2, k + 6  # not multiples of 8
+    rng = np.random.default_rng(12)
+    xbig = rng.standard_normal((m + 1, ldx)).astype(np.float16)
+    wbig = (rng.standard_normal((n + 1, ldw)) * 0.05).astype(np.float16)
+    xd, wd = to_dev(xbig), to_dev(wbig)
+    x_off, w_off = ldx * 2 + 2, 2  # row 1 column 1; row 0 column 1: 2-byte aligned only
+    x = xbig.reshape(-1)[x_off // 2:x_off // 2 + (m - 1) * ldx + k]
+    x = np.stack([x[i * ldx:i * ldx + k] for i in range(m)])
+    w = wbig.reshape(-1)[w_off // 2:w_off // 2 + (n - 1) * ldw + k]
+    w = np.stack([w[j * ldw:j * ldw + k] for j in range(n)])
+    for epi in Epilogue:
+        out_cols = n // 2 if epi == Epilogue.SwigluF16 else n
+        ldy = out_cols + 1  # odd
+        dt = np.float32 if epi in (Epilogue.StoreF32, Epilogue.AddF32) else np.float16
+        y0 = synth.normal_f32(synth.seed_for(402), (m, out_cols), 1.0)
+        ybig = np.full((m + 1, ldy), 3.0, dt)
+        ybig[:m, 1:1 + out_cols] = y0.astype(dt)
+        y = to_dev(ybig)
+        y_off = np.dtype(dt).itemsize  # column 1
+        kernels_ref.gemm.gemm(stream, (xd, x_off), (wd, w_off), (y, y_off), m, n, k, ldx, ldw, ldy, epi)
+        sync()
+        got = to_host(y)[:m, 1:1 + out_cols].astype(np.float32)
+        check_gemm(f"reference unaligned {epi.name}", got,
+                   oracle_epi(x, w, epi, y0.astype(dt).astype(np.float32)))
+        with pytest.raises(AssertionError, match="gemm \\(fast\\)"):
+            kernels.gemm.gemm(stream, (xd, x_off), (wd, w_off), (y, y_off), m, n, k, ldx, ldw, ldy, epi)
+
+
 def test_strides_and_offsets(gpu, kernels, stream):
     """Row strides wider than K / N and operands addressed at byte offsets inside larger buffers,
     as decide's forward does (e.g. the k|v rows of w_in at ATT_K·HIDDEN·2, forward.rs:1157-1158)."""

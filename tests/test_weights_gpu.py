@@ -70,6 +70,11 @@ def _broken(d, tmp_path, edit):
     (lambda ix: ix["tensors"]["L3.w_down"].update(shape=[2560, 9215]), "elements"),
     (lambda ix: ix["tensors"].pop("L3.k_norm"), "no tensor L3.k_norm"),
     (lambda ix: ix["tensors"]["final_norm"].update(offset=1 << 40), "runs past the end"),
+    # 2^64 - 16 KiB is 16 KiB-aligned and exact as a double: offset + bytes would wrap below the blob length
+    (lambda ix: ix["tensors"]["L1.w_gu"].update(offset=(1 << 64) - 16384), "bad offset"),
+    (lambda ix: ix["tensors"]["L1.w_gu"].update(offset=16384.5), "bad offset"),
+    (lambda ix: ix["tensors"]["L3.w_down"].update(shape=[1 << 32, 1 << 32]), "overflows"),
+    (lambda ix: ix["tensors"]["L3.w_down"].update(shape=[2560, 9216.5]), "bad shape"),
     (lambda ix: ix["tensors"]["embed"].update(blob="decide-l99.bin"), "not in the blob list"),
 ])
 def test_loader_refuses_bad_indexes(gpu, kernels, saved, tmp_path, edit, message):
