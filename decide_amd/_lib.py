@@ -83,6 +83,11 @@ PROTOTYPES = {
         [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_uint32, c_uint32,
          c_uint32, c_uint32],
     ),
+    "dh_gemm_nt_noalloc": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_uint32, c_uint32,
+         c_uint32, c_uint32],
+    ),
     "dh_gemm_nt_grouped": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, POINTER(DhGemmMember), c_uint32],

@@ -140,8 +140,10 @@ dh::Plan choose_plan(const dh_ctx* c, uint32_t m, uint32_t n, uint32_t k, uint32
   return dh::plan_gemm(m, n, k, epi, c ? c->ws_cap : (512ull << 20));
 }
 
+// Enqueues plan p. Split-K partials go to `fixed_ws` when given (it must hold
+// p.ws_bytes), else to the context's workspace, grown if needed.
 int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint32_t ldx, uint32_t m, uint32_t k,
-                const dh_gemm_member* mem, uint32_t count) {
+                const dh_gemm_member* mem, uint32_t count, float* fixed_ws = nullptr) {
   dh::TileArgs a{};
   a.x = (const _Float16*)x;
   a.ldx = ldx;
@@ -173,9 +175,13 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
   const uint32_t grid = (uint32_t)grid64;
   if (p.splits > 1) {
     if (count != 1) return fail(DH_EINVAL, "gemm: split-K needs a single member");
-    int rc = ensure_ws(c, p.ws_bytes);
-    if (rc != DH_OK) return rc;
-    a.ws = c->ws;
+    if (fixed_ws) {
+      a.ws = fixed_ws;
+    } else {
+      int rc = ensure_ws(c, p.ws_bytes);
+      if (rc != DH_OK) return rc;
+      a.ws = c->ws;
+    }
   }
   int rc;
   if (stream) {
@@ -187,7 +193,7 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
   }
   if (rc != DH_OK || p.splits == 1) return rc;
   mark(c, kKidReduce);
-  return hip_status(dh::launch_splitk_reduce(c->ws, p.splits, m, mem[0].n, mem[0].y, mem[0].ldy, mem[0].epi, s),
+  return hip_status(dh::launch_splitk_reduce(a.ws, p.splits, m, mem[0].n, mem[0].y, mem[0].ldy, mem[0].epi, s),
                     "split-K reduce launch");
 }
 
@@ -214,9 +220,14 @@ int dh_ctx_create(uint32_t flags, dh_ctx** out) {
   if (e != hipSuccess) return fail(DH_EDEVICE, "dh_ctx_create: hipGetDeviceProperties: %s", hipGetErrorString(e));
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(DH_EDEVICE, "dh_ctx_create: device %d is %s; this library is built for gfx950", dev, prop.gcnArchName);
+  float* scratch = nullptr;
+  e = dh::noalloc_scratch(dev, &scratch);
+  if (e != hipSuccess)
+    return fail(DH_EDEVICE, "dh_ctx_create: no-allocation scratch of device %d: %s", dev, hipGetErrorString(e));
   dh_ctx* c = new dh_ctx();
   c->flags = flags;
   c->device = dev;
+  c->scratch = scratch;
   *out = c;
   return ok();
 }
@@ -249,6 +260,38 @@ int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const voi
   if (p.variant < 0) return fail(DH_EINVAL, "gemm: no plan for M = %u, N = %u, K = %u", m, n, k);
   dh_gemm_member mem{w, y, ldw, ldy, n, epi};
   return launch_plan(ctx, s, p, x, ldx, m, k, &mem, 1);
+}
+
+static_assert(dh::kNoAllocScratchBytes == DH_NOALLOC_SCRATCH_BYTES, "the header states the scratch size");
+
+int dh_gemm_nt_noalloc(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
+                       uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
+  int rc = check_gemm(ctx, x, ldx, w, ldw, y, ldy, m, n, k, epi);
+  if (rc != DH_OK) return rc;
+  if (!ctx) return fail(DH_EINVAL, "gemm (no-alloc): null context");
+  if (!ctx->scratch) return fail(DH_EDEVICE, "gemm (no-alloc): the context has no device scratch");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
+    return fail(DH_EINVAL, "gemm (no-alloc): the context belongs to device %d, device %d is current", ctx->device,
+                dev);
+  hipStream_t s = (hipStream_t)stream;
+  if (ctx->flags & DH_GEMM_REFERENCE) {
+    mark(ctx, kKidReference);
+    return hip_status(dh::launch_gemm_reference((const _Float16*)x, ldx, (const _Float16*)w, ldw, y, ldy, m, n, k,
+                                                epi, s),
+                      "gemm reference kernel launch");
+  }
+  const dh::Plan p = ctx->forced_variant >= 0
+                         ? dh::plan_make(ctx->forced_variant, std::max(1u, ctx->forced_splits), m, n, k, epi)
+                         : dh::plan_gemm(m, n, k, epi, dh::kNoAllocScratchBytes);
+  if (p.variant < 0) return fail(DH_EINVAL, "gemm (no-alloc): no plan for M = %u, N = %u, K = %u", m, n, k);
+  if (p.ws_bytes > dh::kNoAllocScratchBytes)
+    return fail(DH_EINVAL,
+                "gemm (no-alloc): M = %u, N = %u with %u K splits needs %llu bytes of scratch; this entry point "
+                "holds %llu",
+                m, n, p.splits, (unsigned long long)p.ws_bytes, (unsigned long long)dh::kNoAllocScratchBytes);
+  dh_gemm_member mem{w, y, ldw, ldy, n, epi};
+  return launch_plan(ctx, s, p, x, ldx, m, k, &mem, 1, ctx->scratch);
 }
 
 int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, uint32_t m, uint32_t k,

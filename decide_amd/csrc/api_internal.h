@@ -23,6 +23,7 @@ struct dh_ctx {
   // Workspaces a growth replaced. A captured graph holds the raw pointers it was
   // captured with, so superseded buffers stay allocated until dh_ctx_destroy.
   std::vector<void*> retired;
+  float* scratch = nullptr;  // this device's no-allocation scratch (noalloc.hip), kNoAllocScratchBytes
   int forced_variant = -1;
   uint32_t forced_splits = 0;
   std::atomic<uint64_t> used{0};  // bit per distinct kernel launched

@@ -11,6 +11,12 @@ constexpr int kMaxMembers = 8;
 constexpr int kBK = 64;  // K extent of one pipeline stage of the tile kernel
 constexpr uint32_t kSwigluBlock = 16;  // gate|up interleave block (decide's SWIGLU_BLOCK)
 
+// The file-scope device scratch of the no-allocation GEMM entry point
+// (noalloc.hip): split-K partials up to this many bytes.
+constexpr uint64_t kNoAllocScratchBytes = 48ull << 20;
+// Its device address on `device` (which must be current), looked up once per device.
+hipError_t noalloc_scratch(int device, float** out);
+
 // One output of a (grouped) tile launch: Y = epi(X · Wᵀ) for one weight.
 struct Member {
   const _Float16* w;  // [n, k], row stride ldw

@@ -114,6 +114,22 @@ uint32_t dh_variants_loaded(const dh_ctx* ctx);
 int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
                uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
 
+/* The same GEMM without any allocation: no hipMalloc, hipFree or allocating
+ * library call, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid it). decide has no
+ * counterpart. Split-K partials go to a device array of the library, file
+ * scope, DH_NOALLOC_SCRATCH_BYTES on each GPU, which that GPU holds from the
+ * first dh_ctx_create on it until the process ends. The planner picks among
+ * plans whose partials fit it; a forced plan (dh_gemm_force) that needs more
+ * is refused with DH_EINVAL. Same contract and arguments as dh_gemm_nt; the
+ * context's device must be current. Every call on one GPU shares that array
+ * and nothing in it needs clearing (each split-K launch writes every partial
+ * it reads), but calls that overlap on one GPU (different streams, or
+ * different contexts) race on it. */
+#define DH_NOALLOC_SCRATCH_BYTES 50331648u /* 48 MiB */
+int dh_gemm_nt_noalloc(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, void* y,
+                       uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, uint32_t epi);
+
 /* Grouped form: every member shares X (m rows, k columns) and is computed in
  * ONE launch. decide has no grouped call; it fuses members by concatenating
  * their weight rows offline (convert.rs:204-245: qkv|z|b|a, q|gate|k|v,
