@@ -25,10 +25,16 @@
 //     streams from HBM, gets the deeper one; small tiles, whose stages are
 //     short, take 5-deep rings so a DMA has several stages to land). The
 //     DMAs the next stage needs are issued at the start of a stage, the rest
-//     are spread over its MFMAs; one vmcnt wait and one barrier end each stage.
-//   * The hot loop (LDS reads two fragments ahead, MFMAs, waits, DMAs) is
-//     inline asm in program order: accumulators pinned in AGPRs so the
-//     register allocator cannot rotate them, and exact wait counts.
+//     are spread over its MFMAs; one vmcnt wait and one barrier per stage.
+//   * LDS reads just in time (stage_s): per k-half, the operand with fewer
+//     fragments per wave is read whole, the other streamed one fragment per
+//     group of MFMAs, a few groups ahead; the stage's barrier comes before its
+//     last groups, which run from registers while the next stage's first
+//     reads are in flight (tiles with too few fragments per half keep the
+//     read-everything-first schedule, stage()).
+//   * The hot loop (LDS reads, MFMAs, waits, DMAs) is inline asm in program
+//     order: accumulators pinned in AGPRs so the register allocator cannot
+//     rotate them, and exact wait counts.
 //   * K order inside a stage: sub-step s (0, 1) covers k0 + 32s .. +32, and
 //     lane group g = lane / 16 supplies k0 + 32s + 8g .. +8 for both operands.
 //   * M tail in-kernel: rows past M re-read row M-1 (never stored). N tail:
@@ -447,30 +453,135 @@ struct Pipe {
       issue<BX, BW>(kt, nst);
       compute<BX, BW, false, true>(kt);
     }
-    if (kt + 1 < nst) {
-      // DMAs still allowed in flight: this stage's issues not needed by stage kt + 1
-      if (steady) {
-        wait_vm<KEEP>();
-      } else if constexpr (NBX == NBW && NBX > 3) {
-        // near the end of K: the stages kt + 2 .. kt + LA that exist were issued
-        const int later = min(kt + LAX, nst - 1) - (kt + 1);
-        static_for<0, LAX>([&](auto cc) {
-          constexpr int c = decltype(cc)::value;
-          if (later == c) wait_vm<c * (XPW + WPW)>();
-        });
-      } else {
-        const bool ix2 = LAX >= 2 && kt + LAX < nst, iw2 = LAW >= 2 && kt + LAW < nst;
-        if (ix2 && iw2)
-          wait_vm<XPW + WPW>();
-        else if (ix2)
-          wait_vm<XPW>();
-        else if (iw2)
-          wait_vm<WPW>();
-        else
-          wait_vm<0>();
-      }
-    }
+    if (kt + 1 < nst) wait_next(kt, nst, steady);
     __syncthreads();
+  }
+  // Waits until the DMAs stage kt + 1 reads have landed, leaving in flight
+  // only this stage's issues that stage kt + 1 does not need.
+  __device__ __forceinline__ void wait_next(int kt, int nst, bool steady) {
+    if (steady) {
+      wait_vm<KEEP>();
+    } else if constexpr (NBX == NBW && NBX > 3) {
+      // near the end of K: the stages kt + 2 .. kt + LA that exist were issued
+      const int later = min(kt + LAX, nst - 1) - (kt + 1);
+      static_for<0, LAX>([&](auto cc) {
+        constexpr int c = decltype(cc)::value;
+        if (later == c) wait_vm<c * (XPW + WPW)>();
+      });
+    } else {
+      const bool ix2 = LAX >= 2 && kt + LAX < nst, iw2 = LAW >= 2 && kt + LAW < nst;
+      if (ix2 && iw2)
+        wait_vm<XPW + WPW>();
+      else if (ix2)
+        wait_vm<XPW>();
+      else if (iw2)
+        wait_vm<WPW>();
+      else
+        wait_vm<0>();
+    }
+  }
+
+  // ---- The streamed schedule (stage_s): fragments read just in time. ----
+  // Per stage and k-half h, the operand with fewer fragments per wave (R:
+  // X when FM <= FN) is read whole and held for the half; the other (S) is
+  // streamed, one fragment per group of NR MFMAs (group g = (h, s):
+  // acc += R(h, 0..NR-1) x S(h, s)). The stage's LDS reads, in the order the
+  // groups need them, are R(0, *), S(0, *), R(1, *), S(1, *); the reads group g
+  // needs are issued LAG groups ahead (LAG + 1 in the second half, so that all
+  // are out LAG groups before the stage ends). The stage's barrier sits
+  // before its last NB groups: every wave has its reads of this stage back by
+  // then, so after the barrier the next stage's first reads go out while
+  // those last groups run from registers, and the DMAs the next stage issues
+  // may overwrite this stage's slots.
+  static constexpr bool RA = FM <= FN;
+  static constexpr int NR = RA ? FM : FN, NS = RA ? FN : FM;
+  static constexpr int NG = 2 * NS, NL = 2 * (NR + NS);
+  static constexpr int LAG = 3, NB = 3;
+  static constexpr int GB = NG - NB;  // the barrier comes before group GB
+  // used when each half has enough groups for the lookahead (else stage())
+  static constexpr bool STREAMED = NS > LAG + 1 && GB >= 2;
+  // the index (in the stage's read order) of the last read group g needs
+  static constexpr int need(int g) { return (g / NS) * (NR + NS) + NR + g % NS; }
+  // reads issued once group g has issued its own (all of them by group GB - 1)
+  static constexpr int issued(int g) {
+    const int la = g < NS ? LAG : LAG + 1;
+    return need(g + la < NG - 1 ? g + la : NG - 1) + 1;
+  }
+  static constexpr int ENTRY = need(LAG - 1) + 1;  // issued before group 0 (by the previous stage)
+  static_assert(!STREAMED || issued(GB - 1) == NL, "every read of a stage is issued before its barrier");
+
+  h8 rf[2][NR], sf[2][NS];
+
+  // Read I of the stage whose X and W sit in ring slots BX and BW.
+  template <int I, int BX, int BW>
+  __device__ __forceinline__ void read_one() {
+    constexpr int h = I / (NR + NS), q = I % (NR + NS);
+    constexpr bool isr = q < NR;
+    constexpr int f = isr ? q : q - NR;
+    constexpr bool isx = isr == RA;  // an X (A operand) fragment
+    const uint32_t kh = h ? a1 : a0;
+    const uint32_t base = isx ? lds_addr + BX * XBYTES + xrow + kh : lds_addr + WRING + BW * WBYTES + wrow + kh;
+    if constexpr (isr)
+      ds_read16<(isx ? (f % FM) : f) * 16 * 128>(rf[h][f], base);
+    else
+      ds_read16<(isx ? (f % FM) : f) * 16 * 128>(sf[h][f], base);
+  }
+  template <int B, int E, int BX, int BW>
+  __device__ __forceinline__ void read_range() {
+    static_for<B, E>([&](auto ic) { read_one<decltype(ic)::value, BX, BW>(); });
+  }
+  // The first ENTRY reads of the stage in slots (BX, BW).
+  template <int BX, int BW>
+  __device__ __forceinline__ void entry_reads() {
+    read_range<0, ENTRY, BX, BW>();
+  }
+  // Stage kt in ring slots (Q mod NBX, Q mod NBW); its first ENTRY reads were
+  // issued before it.
+  template <int Q>
+  __device__ __forceinline__ void stage_s(int kt, int nst, bool steady) {
+    constexpr int BX = Q % NBX, BW = Q % NBW;
+    constexpr int NX = (Q + 1) % NBX, NW = (Q + 1) % NBW;
+    constexpr int NXS = (BX + LAX) % NBX, NWS = (BW + LAW) % NBW;
+    constexpr int DPW = XPW + WPW;
+    constexpr int NEED = (LAX == 1 ? XPW : 0) + (LAW == 1 ? WPW : 0);  // DMAs stage kt + 1 needs: issued first
+    constexpr int REST = DPW - NEED;
+    if (!steady) issue<BX, BW>(kt, nst);
+    static_for<0, NG>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      constexpr int h = g / NS, s = g % NS;
+      if constexpr (g == GB) {
+        wait_lgkm<0>();
+        if (kt + 1 < nst) wait_next(kt, nst, steady);
+        __syncthreads();
+        if (kt + 1 < nst) entry_reads<NX, NW>();
+      }
+      if constexpr (g < GB) {
+        // this stage's DMAs for stage kt + LA: the ones stage kt + 1 needs at group 0, the rest spread to GB - 1
+        static_for<0, DPW>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          constexpr int dd = (LAX <= LAW) ? d : (d < WPW ? d + XPW : d - WPW);  // issue order
+          constexpr int at = d < NEED ? 0 : 1 + (REST > 0 ? (d - NEED) * (GB - 1) / REST : 0);
+          if constexpr (at == g) {
+            if (steady) dma_one<dd, NXS, NWS>(kt + LAX, kt + LAW);
+          }
+        });
+        read_range<g == 0 ? ENTRY : issued(g - 1), issued(g), BX, BW>();
+        constexpr int pending = issued(g) - need(g) - 1;
+        wait_lgkm<(pending < 15 ? pending : 15)>();
+        tie(sf[h][s]);
+        if constexpr (s == 0) {
+#pragma unroll
+          for (int r = 0; r < NR; ++r) tie(rf[h][r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if constexpr (RA)
+          mfma_acc_v(acc[r][s], rf[h][r], sf[h][s]);
+        else
+          mfma_acc_v(acc[s][r], sf[h][s], rf[h][r]);
+      }
+    });
   }
 };
 
@@ -574,17 +685,26 @@ __device__ __forceinline__ void tile_body(const TileArgs& p) {
         wait_vm<0>();
     }
     __syncthreads();
+    if constexpr (P::STREAMED) pp.template entry_reads<0, 0>();
 
     int kt = 0;
     for (; kt + P::U - 1 + P::LAM < nst; kt += P::U) {
       static_for<0, P::U>([&](auto qc) {
         constexpr int qq = decltype(qc)::value;
-        pp.template stage<qq>(kt + qq, nst, true);
+        if constexpr (P::STREAMED)
+          pp.template stage_s<qq>(kt + qq, nst, true);
+        else
+          pp.template stage<qq>(kt + qq, nst, true);
       });
     }
     static_for<0, P::U + P::LAM>([&](auto qc) {
       constexpr int qq = decltype(qc)::value;
-      if (kt + qq < nst) pp.template stage<qq % P::U>(kt + qq, nst, false);
+      if (kt + qq < nst) {
+        if constexpr (P::STREAMED)
+          pp.template stage_s<qq % P::U>(kt + qq, nst, false);
+        else
+          pp.template stage<qq % P::U>(kt + qq, nst, false);
+      }
     });
   }
 
