@@ -193,10 +193,18 @@ def _attention_case(rows, npos, qpos, seed):
     return q, kc, vc, pq, np.asarray(qpos, np.uint32)
 
 
+# (2307, 2307): config 5's full prompt, 2,307-key causal attention over every row; (70, 1200, "scattered"):
+# positions in no order, so one workgroup's 32 rows reach very different key counts
 @pytest.mark.parametrize("rows,npos,kind", [(37, 37, "prefill"), (300, 300, "prefill"), (3, 900, "answers"),
-                                            (16, 16, "prefill"), (1, 1, "prefill")])
+                                            (16, 16, "prefill"), (1, 1, "prefill"), (2307, 2307, "prefill"),
+                                            (70, 1200, "scattered")])
 def test_attention_matches_oracle(gpu, kernels, stream, rows, npos, kind):
-    qpos = np.arange(rows) if kind == "prefill" else np.array([899, 17, 512])[:rows]
+    if kind == "prefill":
+        qpos = np.arange(rows)
+    elif kind == "answers":
+        qpos = np.array([899, 17, 512])[:rows]
+    else:
+        qpos = np.random.default_rng(7).integers(0, npos, rows)
     q, kc, vc, pq, qpos = _attention_case(rows, npos, qpos, 190)
     y = empty((rows, 4096), np.float16)
     kernels.attn.attention(stream, (to_dev(q), 0), (to_dev(kc), 0), (to_dev(vc), 0), (to_dev(pq), 0), (u32(qpos), 0),
