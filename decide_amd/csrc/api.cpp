@@ -228,6 +228,7 @@ int dh_ctx_create(uint32_t flags, dh_ctx** out) {
   c->flags = flags;
   c->device = dev;
   c->scratch = scratch;
+  c->cus = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : 256u;
   *out = c;
   return ok();
 }
@@ -403,8 +404,11 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
   }
   const bool chunked = (ctx->flags & DH_DELTA_CHUNKED) ||
                        (!(ctx->flags & DH_DELTA_SEQUENTIAL) && max_m >= DH_DELTA_CHUNK_MIN_T);
-  if (chunked) {  // the chunked recurrence's workspace for max_m tokens
-    int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(std::max(1u, max_m)) * sizeof(float));
+  // the forward-kernel workspace: the chunked recurrence's for max_m tokens, attention's key pieces for max_m rows
+  uint64_t aux = dh::attention_ws_max(max_m);
+  if (chunked) aux = std::max<uint64_t>(aux, dh::delta_chunk_ws_floats(std::max(1u, max_m)) * sizeof(float));
+  if (aux) {
+    int rc = ensure_aux(ctx, aux);
     if (rc != DH_OK) return rc;
   }
   // One tiny launch of every tile variant (M = 16, N = bn, K = 64) and of the

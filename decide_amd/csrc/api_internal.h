@@ -18,7 +18,9 @@ struct dh_ctx {
   float* ws = nullptr;
   uint64_t ws_bytes = 0;
   uint64_t ws_cap = 512ull << 20;  // split-K workspace ceiling
-  float* aux = nullptr;            // forward-kernel workspace (the chunked recurrence's per-chunk matrices)
+  uint32_t cus = 256;              // compute units of the device (sizes attention's key pieces)
+  float* aux = nullptr;            // forward-kernel workspace: the chunked recurrence's per-chunk matrices and
+                                   // attention's per-piece partial states (never live at the same time)
   uint64_t aux_bytes = 0;
   // Workspaces a growth replaced. A captured graph holds the raw pointers it was
   // captured with, so superseded buffers stay allocated until dh_ctx_destroy.
@@ -37,7 +39,7 @@ constexpr int kMaxTileVariants = 16;
 enum : int {
   kKidReduce = kMaxTileVariants, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
   kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny,
-  kKidDeltaChunk, kKidStream, kKidCount
+  kKidDeltaChunk, kKidStream, kKidAttnCombine, kKidCount
 };
 static_assert(kKidCount <= 64, "kernel ids must fit dh_ctx::used");
 
@@ -55,5 +57,9 @@ bool aligned(const void* p, uintptr_t a);
 int ensure_aux(dh_ctx* c, uint64_t bytes);
 // The same for the split-K workspace, never beyond c->ws_cap.
 int ensure_ws(dh_ctx* c, uint64_t bytes);
+// dh_attention with a bound on the rows' positions (every qpos[r] < npos), which sizes the key pieces; the
+// forward knows it (the chunk's last position + 1).
+int attention_run(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                  const float* pq, const uint32_t* qpos, uint16_t* y, uint32_t rows, uint32_t ldq, uint32_t npos);
 
 }  // namespace dh_api

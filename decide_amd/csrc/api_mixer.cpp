@@ -15,6 +15,34 @@ constexpr uint32_t kConvDim = 8192, kValueDim = 4096, kNV = 32, kQDim = 4096, kM
 bool misaligned(const void* p, uintptr_t a) { return p && !aligned(p, a); }
 }  // namespace
 
+namespace dh_api {
+
+int attention_run(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                  const float* pq, const uint32_t* qpos, uint16_t* y, uint32_t rows, uint32_t ldq, uint32_t npos) {
+  if (rows < 1) return fail(DH_EINVAL, "attention: rows must be at least 1");
+  if (ldq < 2 * kQDim) return fail(DH_EINVAL, "attention: ldq = %u must cover the gate columns", ldq);
+  if (misaligned(q, 16) || misaligned(kc, 16) || misaligned(vc, 16))
+    return fail(DH_EINVAL, "attention: q, kc and vc must be 16-byte aligned");
+  if (misaligned(pq, 8) || ldq % 2 != 0)
+    return fail(DH_EINVAL, "attention: pq must be 8-byte aligned and ldq = %u even", ldq);
+  if (misaligned(qpos, 4) || misaligned(y, 4)) return fail(DH_EINVAL, "attention: qpos and y must be 4-byte aligned");
+  if (!ctx) return fail(DH_EINVAL, "attention: null context");
+  if (!q || !kc || !vc || !pq || !qpos || !y) return fail(DH_EINVAL, "attention: null pointer");
+  const dh::AttnSplit sp = dh::attention_split(rows, npos, ctx->cus);
+  const uint64_t ws = dh::attention_ws_bytes(rows, sp);
+  if (ws) {  // allocates only past what dh_warm_up sized the workspace for
+    const int rc = ensure_aux(ctx, ws);
+    if (rc != DH_OK) return rc;
+    mark(ctx, kKidAttnCombine);
+  }
+  mark(ctx, kKidAttn);
+  return hip_status(dh::launch_attention((const _Float16*)q, (const _Float16*)kc, (const _Float16*)vc, pq, qpos,
+                                         (_Float16*)y, ws ? ctx->aux : nullptr, rows, ldq, sp, (hipStream_t)stream),
+                    "attention");
+}
+
+}  // namespace dh_api
+
 extern "C" {
 
 int dh_embed_bf16(dh_ctx* ctx, void* stream, const uint32_t* ids, const uint16_t* table, float* out, uint32_t t,
@@ -127,19 +155,9 @@ int dh_kv_norm_rope(dh_ctx* ctx, void* stream, const float* pkv, const float* kw
 
 int dh_attention(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const float* pq,
                  const uint32_t* qpos, uint16_t* y, uint32_t rows, uint32_t ldq) {
-  if (rows < 1) return fail(DH_EINVAL, "attention: rows must be at least 1");
-  if (ldq < 2 * kQDim) return fail(DH_EINVAL, "attention: ldq = %u must cover the gate columns", ldq);
-  if (misaligned(q, 16) || misaligned(kc, 16) || misaligned(vc, 16))
-    return fail(DH_EINVAL, "attention: q, kc and vc must be 16-byte aligned");
-  if (misaligned(pq, 8) || ldq % 2 != 0)
-    return fail(DH_EINVAL, "attention: pq must be 8-byte aligned and ldq = %u even", ldq);
-  if (misaligned(qpos, 4) || misaligned(y, 4)) return fail(DH_EINVAL, "attention: qpos and y must be 4-byte aligned");
-  if (!ctx) return fail(DH_EINVAL, "attention: null context");
-  if (!q || !kc || !vc || !pq || !qpos || !y) return fail(DH_EINVAL, "attention: null pointer");
-  mark(ctx, kKidAttn);
-  return hip_status(dh::launch_attention((const _Float16*)q, (const _Float16*)kc, (const _Float16*)vc, pq, qpos,
-                                         (_Float16*)y, rows, ldq, (hipStream_t)stream),
-                    "attention");
+  // decide's interface carries no cache length: the key pieces are sized as if the rows were a prompt's first
+  // `rows` positions (any positions stay correct; only the load balance assumes it)
+  return attention_run(ctx, stream, q, kc, vc, pq, qpos, y, rows, ldq, rows);
 }
 
 int dh_fill_normal(dh_ctx* ctx, void* stream, void* out, uint64_t n, uint64_t seed, float mean, float std,

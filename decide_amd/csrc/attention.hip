@@ -25,10 +25,20 @@
 //     O is rescaled) only when a score passes it by more than 2^8, which after
 //     the first blocks almost never happens. Blocks wholly before every row of
 //     the wave skip the causal mask.
-//   * Query blocks run longest-first so the causal triangle's tail is not
-//     the last work scheduled. Rows past `rows` are clamped for loads and
-//     skipped for stores; keys past the block's last position are masked
-//     (their staged rows are clamped reads of valid cache rows).
+//   * One workgroup per CU (two waves per SIMD), so a causal prompt's longest
+//     query block (all of its keys) would set the kernel's time while most
+//     CUs sit idle. A query block's keys are therefore cut into pieces of L
+//     key blocks at fixed offsets (piece p covers blocks [pL, pL + L), the
+//     last piece the rest), one workgroup each, dispatched longest-first;
+//     a query block with more than one piece writes each piece's (max,
+//     sum, unnormalised O) per row and head, and attention_combine_kernel
+//     merges them. The cut points depend only on L (chosen on the host from
+//     the row count and the key bound), never on the neighbouring rows, so a
+//     row whose keys end before a cut gets bit for bit the one-piece result.
+//   * Rows past `rows` are clamped for loads and skipped for stores; keys past
+//     the block's last position are masked (their staged rows are clamped
+//     reads of valid cache rows).
+#include <algorithm>
 #include <type_traits>
 
 #include "dh_kernels.h"
@@ -74,15 +84,37 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
 }
 }  // namespace
 
+// The largest position over query block qb's 32 rows (rows past `rows` clamped
+// to the last one): its last key, the same in both kernels.
+__device__ __forceinline__ uint32_t block_kmax(const uint32_t* __restrict__ qpos, uint32_t qb, uint32_t rows,
+                                               uint32_t lane) {
+  uint32_t v = qpos[min(qb * kBQ + (lane & 31), rows - 1)];
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
+// Pieces query block qb really has: ceil(nblk / L), at most np (the last one
+// takes the remainder).
+__device__ __forceinline__ uint32_t block_pieces(uint32_t nblk, uint32_t L, uint32_t np) {
+  return min(np, (nblk + L - 1) / L);
+}
+
 __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ kc,
                                                         const _Float16* __restrict__ vc, const float* __restrict__ pq,
                                                         const uint32_t* __restrict__ qpos, _Float16* __restrict__ y,
-                                                        uint32_t ldq, uint32_t rows) {
+                                                        float* __restrict__ part, uint32_t ldq, uint32_t rows,
+                                                        uint32_t L, uint32_t np) {
   __shared__ __attribute__((aligned(16))) _Float16 ks[kBKey * kKLD];
   __shared__ __attribute__((aligned(16))) _Float16 vts[kHD * kVLD];
   __shared__ uint32_t wpmax[8];
-  const uint32_t qb = gridDim.x - 1 - blockIdx.x;
-  const uint32_t kvh = blockIdx.y;
+  // Work item: kv head fastest, then query blocks longest (last) first, then pieces. The hardware deals
+  // workgroups round-robin over the 8 XCDs, so each XCD gets every 8th item: with pieces outermost, any 8
+  // consecutive items are two query blocks' worth of the same piece, of about the same length.
+  const uint32_t nqb = (rows + kBQ - 1) / kBQ;
+  const uint32_t kvh = blockIdx.x & 3;
+  const uint32_t qb = nqb - 1 - (blockIdx.x >> 2) % nqb;
+  const uint32_t piece = (blockIdx.x >> 2) / nqb;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t h = kvh * 4 + (wave & 3);
   const int rl = lane & 15, g = lane >> 4;
@@ -111,6 +143,12 @@ __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restri
   for (int i = 1; i < 8; ++i) kmax = max(kmax, wpmax[i]);
 
   const uint32_t nblk = kmax / kBKey + 1;
+  const uint32_t npieces = block_pieces(nblk, L, np);
+  if (piece >= npieces) return;  // uniform over the workgroup: every wave read the same kmax
+  // this piece's key blocks: L of them (L even, so the pair loop below covers them exactly), the last piece the
+  // rest (its pair loop may run one block past nblk, which is wholly masked)
+  const uint32_t b0 = piece * L;
+  const uint32_t b1 = piece + 1 == npieces ? nblk : b0 + L;
   // staging: K rows as 16-byte chunks (thread → key id / 32, chunk id % 32, two per thread);
   // V as key pairs × 8-dim chunks, transposed into vts on the way in
   const int kp = tid & 15, dc = tid >> 4;
@@ -195,14 +233,31 @@ __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restri
   // branch there makes it wait for every load at the loop head). A block past the last one (odd nblk)
   // stages clamped rows whose keys are all masked: its scores are -inf, its weights 0 and alpha 1,
   // so it changes nothing.
-  fetch(0, std::integral_constant<int, 0>{});
-  fetch(kBKey, std::integral_constant<int, 1>{});
-  for (uint32_t blk = 0; blk < nblk; blk += 2) {
+  fetch(b0 * kBKey, std::integral_constant<int, 0>{});
+  fetch((b0 + 1) * kBKey, std::integral_constant<int, 1>{});
+  for (uint32_t blk = b0; blk < b1; blk += 2) {
     block(blk, std::integral_constant<int, 0>{});
     block(blk + 1, std::integral_constant<int, 1>{});
   }
 
   const float l = sum4_rows(lsum);
+  if (npieces > 1) {
+    // This piece's state for the combine: O unnormalised (relative to m), and (m, l), where a row with no key in
+    // the piece (position before its first key) has weights of exp2(0) on masked scores: its l is written as 0
+    // and the combine skips the piece for that row by the same position test.
+    if (r0 + rl < rows) {
+      const uint32_t prow = nqb * kBQ;
+      const size_t slot = ((size_t)piece * prow + r0 + rl) * kNQ + h;
+      float* op = part + slot * kHD;
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) *(f4*)(op + 16 * dt + 4 * g) = oacc[dt];
+      if (g == 0) {
+        float* ml = part + (size_t)np * prow * kNQ * kHD + 2 * slot;
+        *(f2*)ml = f2{m, (uint64_t)mypos >= (uint64_t)b0 * kBKey ? l : 0.0f};
+      }
+    }
+    return;
+  }
   const float inv = 1.0f / l;
   if (r0 + rl < rows) {
     const uint32_t r = r0 + rl;
@@ -223,11 +278,130 @@ __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restri
   }
 }
 
+// Merges the pieces of every query block that has more than one: a workgroup
+// per row, a lane per (query head, 16 dims). Only the pieces whose first key
+// the row can see take part (the attention kernel's position test); with one
+// such piece the arithmetic is the one-piece path's own (weight exp2(0) = 1),
+// so the result is identical.
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ part,
+                                                                const float* __restrict__ pq,
+                                                                const uint32_t* __restrict__ qpos,
+                                                                _Float16* __restrict__ y, uint32_t ldq, uint32_t rows,
+                                                                uint32_t L, uint32_t np) {
+  const uint32_t r = blockIdx.x, qb = r / kBQ;
+  const int tid = threadIdx.x;
+  const uint32_t kmax = block_kmax(qpos, qb, rows, tid & 63);
+  const uint32_t npieces = block_pieces(kmax / kBKey + 1, L, np);
+  if (npieces <= 1) return;  // written by the attention kernel itself
+  const uint32_t mypos = qpos[r];
+  const uint32_t nv = (uint32_t)min((uint64_t)npieces, (uint64_t)mypos / ((uint64_t)L * kBKey) + 1);
+  const uint32_t h = tid >> 4, d0 = 16 * (tid & 15);
+  const uint32_t prow = (rows + kBQ - 1) / kBQ * kBQ;
+  const size_t pstride = (size_t)prow * kNQ;  // (row, head) slots per piece
+  const size_t slot0 = (size_t)r * kNQ + h;
+  const float* ml = part + (size_t)np * pstride * kHD;
+  float mv[kAttnMaxPieces], lv[kAttnMaxPieces];
+#pragma unroll
+  for (uint32_t p = 0; p < kAttnMaxPieces; ++p)
+    if (p < nv) {
+      const f2 st = *(const f2*)(ml + 2 * (p * pstride + slot0));
+      mv[p] = st[0];
+      lv[p] = st[1];
+    }
+  float mx = mv[0];
+#pragma unroll
+  for (uint32_t p = 1; p < kAttnMaxPieces; ++p)
+    if (p < nv) mx = fmaxf(mx, mv[p]);
+  f4 o[4];
+  float l;
+  {  // piece 0 holds every row's first key
+    const float w = exp2f(mv[0] - mx);
+    const f4* op = (const f4*)(part + slot0 * kHD + d0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = op[j] * w;
+    l = lv[0] * w;
+  }
+#pragma unroll
+  for (uint32_t p = 1; p < kAttnMaxPieces; ++p)
+    if (p < nv) {
+      const float w = exp2f(mv[p] - mx);
+      const f4* op = (const f4*)(part + (p * pstride + slot0) * kHD + d0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] += op[j] * w;
+      l += lv[p] * w;
+    }
+  const float inv = 1.0f / l;
+  const float* gp = pq + (size_t)r * ldq + kQDim + h * kHD + d0;
+  _Float16* yp = y + (size_t)r * kQDim + h * kHD + d0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const f2 gt = *(const f2*)(gp + 2 * j);
+    const float o0 = o[j / 2][2 * (j % 2)], o1 = o[j / 2][2 * (j % 2) + 1];
+    *(h2*)(yp + 2 * j) = h2{(_Float16)(o0 * inv * (1.0f / (1.0f + __expf(-gt[0])))),
+                            (_Float16)(o1 * inv * (1.0f / (1.0f + __expf(-gt[1]))))};
+  }
+}
+
+AttnSplit attention_split(uint32_t rows, uint32_t npos, uint32_t cus) {
+  AttnSplit sp;
+  if (rows == 0) return sp;
+  npos = std::max(npos, rows);
+  const uint32_t nqb = (rows + kBQ - 1) / kBQ;
+  const uint32_t nbm = (npos + kBKey - 1) / kBKey;  // key blocks of the furthest row
+  // key blocks over every query block if the rows sit at positions npos - rows .. npos - 1 (a prompt chunk)
+  uint64_t est = 0;
+  for (uint32_t qb = 0; qb < nqb; ++qb) {
+    const uint64_t last = std::min<uint64_t>(npos - 1, (uint64_t)(npos - rows) + (uint64_t)qb * kBQ + kBQ - 1);
+    est += last / kBKey + 1;
+  }
+  // Pieces of 1.3x one CU's even share of the work (4 kv heads), even length, at most kAttnMaxPieceRows / 32
+  // query-block pieces in all (the workspace bound). Measured at 2,307 causal rows: 1.0x (L = 44 blocks)
+  // 125 us, 1.3x (L = 56) 113 us, 1.5x (L = 64) 122 us; at 1,024 rows 1.3x is also the fastest. Fewer, longer
+  // pieces write fewer partial states for the combine; shorter ones balance the CUs better.
+  auto even_up = [](uint64_t v) { return (uint32_t)std::max<uint64_t>(2, (v + 1) & ~1ull); };
+  const uint32_t cap = std::min<uint32_t>(kAttnMaxPieces, std::max<uint32_t>(1, kAttnMaxPieceRows / kBQ / nqb));
+  uint32_t L = even_up((est * 4 * 13 / 10 + cus - 1) / std::max(1u, cus));
+  uint32_t np = (nbm + L - 1) / L;
+  if (np > cap) {
+    L = even_up((nbm + cap - 1) / cap);
+    np = (nbm + L - 1) / L;
+  }
+  if (np <= 1) return sp;
+  sp.L = L;
+  sp.np = np;
+  return sp;
+}
+
+uint64_t attention_ws_bytes(uint32_t rows, const AttnSplit& sp) {
+  if (sp.np <= 1) return 0;
+  const uint64_t prow = (uint64_t)(rows + kBQ - 1) / kBQ * kBQ;
+  return (uint64_t)sp.np * prow * kNQ * (kHD + 2) * sizeof(float);
+}
+
+uint64_t attention_ws_max(uint32_t max_rows) {
+  uint64_t most = 0;
+  for (uint32_t nqb = 1; nqb <= (std::max(1u, max_rows) + kBQ - 1) / kBQ; ++nqb) {
+    AttnSplit sp;
+    sp.np = std::min<uint32_t>(kAttnMaxPieces, std::max<uint32_t>(1, kAttnMaxPieceRows / kBQ / nqb));
+    most = std::max(most, attention_ws_bytes(nqb * kBQ, sp));
+  }
+  return most;
+}
+
 hipError_t launch_attention(const _Float16* q, const _Float16* kc, const _Float16* vc, const float* pq,
-                            const uint32_t* qpos, _Float16* y, uint32_t rows, uint32_t ldq, hipStream_t s) {
+                            const uint32_t* qpos, _Float16* y, float* part, uint32_t rows, uint32_t ldq,
+                            const AttnSplit& sp, hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(attention_kernel, dim3((rows + kBQ - 1) / kBQ, 4), dim3(512), 0, s, q, kc, vc, pq, qpos, y, ldq,
-                     rows);
+  if (sp.np == 0 || sp.L == 0 || sp.L % 2 != 0 || (sp.np > 1 && !part)) return hipErrorInvalidValue;
+  const uint32_t nqb = (rows + kBQ - 1) / kBQ;
+  hipLaunchKernelGGL(attention_kernel, dim3(nqb * sp.np * 4), dim3(512), 0, s, q, kc, vc, pq, qpos, y, part, ldq,
+                     rows, sp.L, sp.np);
+  if (sp.np > 1) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(rows), dim3(256), 0, s, part, pq, qpos, y, ldq, rows, sp.L,
+                       sp.np);
+  }
   return hipGetLastError();
 }
 

@@ -101,8 +101,23 @@ hipError_t launch_q_norm_rope(const float* pq, const float* qw, const float* inv
 hipError_t launch_kv_norm_rope(const float* pkv, const float* kw, const float* inv_freq, _Float16* kc, _Float16* vc,
                                uint32_t rows, uint32_t ldkv, uint32_t kcol, uint32_t vcol, uint32_t pos0,
                                hipStream_t s);
+// Attention's key pieces: each query block's keys are cut every L blocks of 32
+// keys into at most np pieces (np = 1: no cut, no workspace).
+struct AttnSplit {
+  uint32_t L = 2;
+  uint32_t np = 1;
+};
+constexpr uint32_t kAttnMaxPieces = 16;       // pieces per query block
+constexpr uint32_t kAttnMaxPieceRows = 5120;  // query-block rows x pieces with partial state (the workspace bound)
+// The cut for `rows` query rows whose positions are below npos, on `cus` CUs.
+AttnSplit attention_split(uint32_t rows, uint32_t npos, uint32_t cus);
+// Workspace bytes the cut needs (the pieces' partial states), 0 for np = 1.
+uint64_t attention_ws_bytes(uint32_t rows, const AttnSplit& sp);
+// The most any cut for up to max_rows query rows can need (at most 84.5 MB).
+uint64_t attention_ws_max(uint32_t max_rows);
 hipError_t launch_attention(const _Float16* q, const _Float16* kc, const _Float16* vc, const float* pq,
-                            const uint32_t* qpos, _Float16* y, uint32_t rows, uint32_t ldq, hipStream_t s);
+                            const uint32_t* qpos, _Float16* y, float* part, uint32_t rows, uint32_t ldq,
+                            const AttnSplit& sp, hipStream_t s);
 hipError_t launch_embed_bf16(const uint32_t* ids, const uint16_t* table, float* out, uint32_t t, uint32_t h,
                              hipStream_t s);
 

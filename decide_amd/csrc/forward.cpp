@@ -159,8 +159,9 @@ int layer_full(dh_model* m, void* s, const Layer& L, const Chunk& ch, Source src
                        ATT_IN_N));
     TRY(dh_kv_norm_rope(m->ctx, s, m->p, as<float>(L.k_norm->ptr), m->inv_freq, (uint16_t*)m->kc[L.att_index],
                         (uint16_t*)m->vc[L.att_index], rows, ATT_IN_N, ATT_K, ATT_V, ch.pos0));
-    TRY(dh_attention(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
-                     (const uint16_t*)m->vc[L.att_index], m->p, qpos, (uint16_t*)m->g, rows, ATT_IN_N));
+    TRY(dh_api::attention_run(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
+                              (const uint16_t*)m->vc[L.att_index], m->p, qpos, (uint16_t*)m->g, rows, ATT_IN_N,
+                              ch.pos0 + rows));
   }
   TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, m->x, HIDDEN, rows, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
   return mlp(m, s, L, m->x, m->h, rows);
@@ -195,8 +196,10 @@ int layer_pruned(dh_model* m, void* s, const Layer& L, const RunArgs& r, const C
   // rows 0..ATT_K of w_in are q|gate
   TRY(gemm(m, s, hs, HIDDEN, w_in, HIDDEN, ps, ATT_K, n, ATT_K, HIDDEN, DH_EPI_STORE_F32));
   TRY(dh_q_norm_rope(m->ctx, s, ps, as<float>(L.q_norm->ptr), m->inv_freq, qpos, (uint16_t*)m->qo, n, ATT_K));
-  TRY(dh_attention(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
-                   (const uint16_t*)m->vc[L.att_index], ps, qpos, (uint16_t*)m->g, n, ATT_K));
+  // the answers sit at positions below the chunk's end
+  TRY(dh_api::attention_run(m->ctx, s, (const uint16_t*)m->qo, (const uint16_t*)m->kc[L.att_index],
+                            (const uint16_t*)m->vc[L.att_index], ps, qpos, (uint16_t*)m->g, n, ATT_K,
+                            ch.pos0 + ch.rows));
   TRY(dh_gather_rows_f32(m->ctx, s, m->x, rowmap, xs, n, HIDDEN));
   TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, xs, HIDDEN, n, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
   TRY(mlp(m, s, L, xs, hs, n));

@@ -193,11 +193,13 @@ def _attention_case(rows, npos, qpos, seed):
     return q, kc, vc, pq, np.asarray(qpos, np.uint32)
 
 
-# (2307, 2307): config 5's full prompt, 2,307-key causal attention over every row; (70, 1200, "scattered"):
-# positions in no order, so one workgroup's 32 rows reach very different key counts
+# (2307, 2307): config 5's full prompt, 2,307-key causal attention over every row, its long query blocks cut into
+# two key pieces; (70, 1200, "scattered"): positions in no order, so one workgroup's 32 rows reach very different
+# key counts; (600, 2307, "scattered"): every query block cut into five pieces, the last one long, with rows that
+# see no key of some pieces; (300, 300): five pieces per query block
 @pytest.mark.parametrize("rows,npos,kind", [(37, 37, "prefill"), (300, 300, "prefill"), (3, 900, "answers"),
                                             (16, 16, "prefill"), (1, 1, "prefill"), (2307, 2307, "prefill"),
-                                            (70, 1200, "scattered")])
+                                            (70, 1200, "scattered"), (600, 2307, "scattered")])
 def test_attention_matches_oracle(gpu, kernels, stream, rows, npos, kind):
     if kind == "prefill":
         qpos = np.arange(rows)
@@ -215,6 +217,35 @@ def test_attention_matches_oracle(gpu, kernels, stream, rows, npos, kind):
     assert np.isfinite(got).all()
     e = orc.rel_frobenius(got, want)
     assert e <= 2e-3, f"attention rel. Frobenius {e:.2e}"  # fp16 P operand and fp16 output
+
+
+def test_attention_key_pieces_keep_rows_independent(gpu, kernels, stream):
+    """96 rows at scattered positions: their query blocks' keys are cut into pieces (every 64 keys at the shortest)
+    and merged. A row whose position is below 64 sees one piece only and gets bit for bit the result of a call
+    with that row alone (never cut); a row past it matches the one-row call within one fp16 rounding."""
+    rows = 96
+    qpos = np.random.default_rng(11).integers(0, 1200, rows)
+    qpos[::7] = np.arange(0, 64, 64 / len(qpos[::7])).astype(np.int64)[:len(qpos[::7])]
+    q, kc, vc, pq, qpos = _attention_case(rows, 1200, qpos, 210)
+    y = empty((rows, 4096), np.float16)
+    args = ((to_dev(kc), 0), (to_dev(vc), 0))
+    kernels.attn.attention(stream, (to_dev(q), 0), *args, (to_dev(pq), 0), (u32(qpos), 0), (y, 0), rows, ATT_IN_N)
+    sync()
+    got = to_host(y)
+    early = [r for r in range(rows) if qpos[r] < 64]
+    late = [r for r in range(rows) if qpos[r] >= 64][:12]
+    assert len(early) >= 8 and len(late) == 12
+    for r in early + late:
+        y1 = empty((1, 4096), np.float16)
+        kernels.attn.attention(stream, (to_dev(q[r:r + 1]), 0), *args, (to_dev(pq[r:r + 1]), 0),
+                               (u32(qpos[r:r + 1]), 0), (y1, 0), 1, ATT_IN_N)
+        sync()
+        one = to_host(y1)[0]
+        if qpos[r] < 64:
+            np.testing.assert_array_equal(got[r], one, err_msg=f"row {r} at {qpos[r]}")
+        else:
+            np.testing.assert_allclose(got[r].astype(np.float32), one.astype(np.float32), rtol=1e-3, atol=1e-4,
+                                       err_msg=f"row {r} at {qpos[r]}")
 
 
 def test_attention_rows_are_independent_of_their_neighbours(gpu, kernels, stream):
