@@ -12,11 +12,11 @@
 //   V' = U − W Sᵀ,   S ← γ_C S + V'ᵀ diag(γ_C/γ) K,
 // and, for every chunk independently once its S and V' are known,
 //   O = diag(γ) Q Sᵀ + M V'.
-// Three kernels:
+// Two kernels:
 //   prep: W, U, M and K̃ᵀ = (diag(γ_C/γ) K)ᵀ for every (chunk, value head);
 //   scan: the chunks in order for each (head, 16 value rows), keeping the
-//         state slice in LDS; it stores each chunk's starting S and V';
-//   out:  O for every (chunk, head, 32 value columns).
+//         state slice in LDS, and O for those rows from each chunk's
+//         starting S and V' while the next state is being formed.
 // Tokens past T in the last chunk enter with k = q = v = 0, β = 0 and
 // log g = 0, so they change nothing.
 //
@@ -42,9 +42,7 @@ constexpr int kOffU = kOffW + C * DK;     // U [64][128]
 constexpr int kOffM = kOffU + C * DK;     // M [64][64]
 constexpr int kOffKt = kOffM + C * C;     // K̃ᵀ [128][64]
 constexpr int kOffGam = kOffKt + DK * C;  // γ [64]
-constexpr int kOffVt = kOffGam + C;       // V'ᵀ [128][64] (scan → out)
-constexpr int kOffS = kOffVt + DV * C;    // S at the chunk start [128][128] (scan → out)
-constexpr int kWsStride = kOffS + DV * DK;
+constexpr int kWsStride = kOffGam + C;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -300,20 +298,25 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
 // ---------------------------------------------------------------------------
 // scan: one workgroup per (value head, 16 value rows); the 8 workgroups of a
 // head have ids 32 apart, so they run on one XCD and share its L2 for the
-// per-chunk matrices. Waves 0-3 compute and touch LDS only; wave 4 does all
-// the global memory work, so that its issue stalls never hold up an MFMA:
+// per-chunk matrices. Waves 0-3 carry the recurrence and touch LDS only;
+// waves 4-7 ("out waves", one per 16 tokens of the chunk) do all the global
+// memory work and the chunk's output, so their stalls never hold up the
+// recurrence's MFMAs:
 //   chunk c, waves 0-3:  V'ᵀ = Uᵀ − S Wᵀ (wave w: tokens 16 w .. + 16)
 //                        | barrier |
 //                        S = γ_C S + V'ᵀ K̃ (wave w: key columns 32 w .. + 32)
-//   chunk c, wave 4:     DMA chunk c + 1's W, K̃ᵀ and U slice into the other
-//                        LDS buffer; store S (the chunk's starting state)
+//   chunk c, waves 4-7:  DMA a quarter of chunk c + 1's W, K̃ᵀ and U slice
+//                        into the other LDS buffer; X = Q Sᵀ for their
+//                        tokens (S is still the chunk's starting state)
 //                        | barrier |
-//                        store V'ᵀ; wait for the DMA
+//                        O = diag(γ) X + M V' (V' complete), stored; wait
+//                        for the DMA
 //   | barrier |
 // W and K̃ᵀ land by global→LDS DMA (16 bytes per lane, 1 KB per instruction)
 // in an unpadded layout whose 16-byte chunks are XOR-swizzled by row
 // (chunk c of row r at c ^ (r % 16)), so the MFMA operand reads stay
-// conflict-free.
+// conflict-free. An out wave's Q and M rows go straight into registers, in
+// the MFMA's k layout, one chunk ahead.
 constexpr int kScanRows = 16;
 
 // Wave-uniform copies in SGPRs (the DMA below takes its LDS address and its
@@ -375,95 +378,145 @@ __device__ __forceinline__ f4 nt_tile_swz(const float* A, int lda, const float* 
   return acc + acc2;
 }
 
-__global__ __launch_bounds__(320) void delta_chunk_scan_kernel(float* __restrict__ ws, const float* state_in,
-                                                               float* state_out, uint32_t T, uint32_t write_state) {
+__global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict__ ws, const float* __restrict__ q,
+                                                               const float* state_in, float* state_out,
+                                                               float* __restrict__ o, uint32_t T,
+                                                               uint32_t write_state) {
   __shared__ __attribute__((aligned(16))) float Ss[kScanRows * LDF];
   __shared__ __attribute__((aligned(1024))) float Wb[2][C * DK];   // [64 tokens][32 chunks], swizzled
   __shared__ __attribute__((aligned(1024))) float Kb[2][DK * C];   // [128 keys][16 chunks], swizzled
   __shared__ __attribute__((aligned(1024))) float Ub[2][C * kScanRows];  // [64 tokens][16 values]
   __shared__ __attribute__((aligned(16))) float Vt[kScanRows * LDT];
   __shared__ float Gc[2];
-  const uint32_t h = blockIdx.x, dv0 = blockIdx.y * kScanRows;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t h = blockIdx.x, hk = h >> 1, dv0 = blockIdx.y * kScanRows;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // in an SGPR: the DMA's LDS offsets derive from it
   const int r = lane & 15, g = lane >> 4;
   const uint32_t nch = (T + C - 1) / C;
   auto slot = [&](uint32_t c) { return ws + ((size_t)c * NV + h) * kWsStride; };
 
-  // wave 4: chunk c's W, K̃ᵀ and U slice into buffer bf by DMA
-  auto dma_chunk = [&](uint32_t c, int bf) {
+  // out wave ow's quarter of chunk c's W, K̃ᵀ and U slice into buffer bf by DMA
+  auto dma_chunk = [&](uint32_t c, int bf, int ow) {
     const float* in = slot(c);
     const uint64_t bw = sgpr_ptr(in + kOffW), bk = sgpr_ptr(in + kOffKt), bu = sgpr_ptr(in + kOffU);
     const uint32_t wl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Wb[bf]);
     const uint32_t kl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Kb[bf]);
     const uint32_t ul = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Ub[bf]);
+    const int n0 = 8 * ow;
     // W: LDS chunk 64 n + lane = row 2 n + lane / 32, slot lane % 32
     auto dma_w = [&](int n) {
       const int row = 2 * n + (lane >> 5), c4 = (lane & 31) ^ (row & 15);
       return (uint32_t)((row * DK + 4 * c4) * 4);
     };
-    dma16_lds<true>(wl, dma_w(0), bw);
-#pragma unroll 4
-    for (int n = 1; n < 32; ++n) dma16_lds(wl + n * 1024, dma_w(n), bw);
+    dma16_lds<true>(wl + n0 * 1024, dma_w(n0), bw);
+#pragma unroll
+    for (int n = 1; n < 8; ++n) dma16_lds(wl + (n0 + n) * 1024, dma_w(n0 + n), bw);
     // K̃ᵀ: row 4 n + lane / 16, slot lane % 16
     auto dma_k = [&](int n) {
       const int row = 4 * n + (lane >> 4), c4 = (lane & 15) ^ (row & 15);
       return (uint32_t)((row * C + 4 * c4) * 4);
     };
-    dma16_lds<true>(kl, dma_k(0), bk);
-#pragma unroll 4
-    for (int n = 1; n < 32; ++n) dma16_lds(kl + n * 1024, dma_k(n), bk);
-    // U rows, columns dv0 .. + 16: row 16 n + lane / 4, chunk lane % 4
-    auto dma_u = [&](int n) { return (uint32_t)(((16 * n + (lane >> 2)) * DK + dv0 + 4 * (lane & 3)) * 4); };
-    dma16_lds<true>(ul, dma_u(0), bu);
 #pragma unroll
-    for (int n = 1; n < 4; ++n) dma16_lds(ul + n * 1024, dma_u(n), bu);
+    for (int n = 0; n < 8; ++n) dma16_lds(kl + (n0 + n) * 1024, dma_k(n0 + n), bk);
+    // U rows, columns dv0 .. + 16: row 16 n + lane / 4, chunk lane % 4
+    dma16_lds(ul + ow * 1024, (uint32_t)(((16 * ow + (lane >> 2)) * DK + dv0 + 4 * (lane & 3)) * 4), bu);
+  };
+  // an out wave's operands for chunk c: Q[t0 + i0 + r][32 g .. + 32], M[i0 + r][16 jb + 4 g .. + 4] (jb ≤ ow), and
+  // γ of the tokens its output lanes hold
+  const int ow = wave - 4, i0 = 16 * ow;
+  f4 qa[8], ma[4], gi;  // this chunk's
+  f4 qn[8], mn[4], gn;  // the next chunk's, loaded during this one
+  auto load_ops = [&](uint32_t c) {
+    const uint32_t t = c * C + i0 + r;
+    const float* qr = q + ((size_t)min(t, T - 1) * NK + hk) * DK + 32 * g;  // rows past T: any finite row
+#pragma unroll
+    for (int n = 0; n < 8; ++n) qn[n] = *(const f4*)(qr + 4 * n);
+    gn = *(const f4*)(slot(c) + kOffGam + i0 + 4 * g);
+    const float* mr = slot(c) + kOffM + (i0 + r) * C + 4 * g;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) mn[jb] = jb <= ow ? *(const f4*)(mr + 16 * jb) : f4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto take_ops = [&]() {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) qa[n] = qn[n];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) ma[jb] = mn[jb];
+    gi = gn;
   };
 
-  if (wave == 4) {
-    dma_chunk(0, 0);
+  if (wave >= 4) {
+    dma_chunk(0, 0, ow);
+    load_ops(0);
     const float gc = slot(0)[kOffGam + C - 1];
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (lane == 0) Gc[0] = gc;
+    take_ops();
+    if (wave == 4 && lane == 0) Gc[0] = gc;
   } else {
     for (int e = tid; e < kScanRows * DK / 4; e += 256) {
       const int row = e >> 5, d4 = (e & 31) * 4;
       *(f4*)(Ss + row * LDF + d4) = *(const f4*)(state_in + ((size_t)h * DV + dv0 + row) * DK + d4);
     }
+    // the recurrence's waves issue first when both waves of a SIMD are ready: the out waves fill the gaps
+    __builtin_amdgcn_s_setprio(3);
   }
   __syncthreads();
 
   for (uint32_t c = 0; c < nch; ++c) {
     const int bf = c & 1;
-    float* io = slot(c);
     float gc_next = 0.f;
-    if (wave == 4) {
+    f4 x;
+    if (wave >= 4) {
       if (c + 1 < nch) {
-        dma_chunk(c + 1, bf ^ 1);  // buffer bf ^ 1 was last read during chunk c - 1
-        gc_next = slot(c + 1)[kOffGam + C - 1];
+        dma_chunk(c + 1, bf ^ 1, ow);  // buffer bf ^ 1 was last read during chunk c - 1
+        if (wave == 4) gc_next = slot(c + 1)[kOffGam + C - 1];
+        load_ops(c + 1);
       }
+      // X[i][dv] = Σ_d Q[i][d] S[dv][d] with S the chunk's starting state
+      f4 sb[8];
+      const float* sr = Ss + r * LDF + 32 * g;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {  // the chunk's starting S slice, for `out`
-        const int idx = 64 * n + lane, row = idx >> 5, c4 = idx & 31;
-        *(f4*)(io + kOffS + (dv0 + row) * DK + 4 * c4) = *(const f4*)(Ss + row * LDF + 4 * c4);
-      }
+      for (int n = 0; n < 8; ++n) sb[n] = *(const f4*)(sr + 4 * n);
+      __builtin_amdgcn_sched_barrier(0);
+      f4 x2 = f4{0.f, 0.f, 0.f, 0.f};
+      x = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          x = mfma4(qa[n][e], sb[n][e], x);
+          x2 = mfma4(qa[n][e + 1], sb[n][e + 1], x2);
+        }
+      x = (x + x2) * gi;
     } else {  // V'ᵀ[dv][i] = U[i][dv] − Σ_d S[dv][d] W[i][d]
-      const int i0 = 16 * wave;
-      const f4 acc = nt_tile_swz<DK, 32>(Ss, LDF, Wb[bf], i0, r, g, f4{0.f, 0.f, 0.f, 0.f});
+      const int iw = 16 * wave;
+      const f4 acc = nt_tile_swz<DK, 32>(Ss, LDF, Wb[bf], iw, r, g, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int dv = 4 * g + e, i = i0 + r;
+        const int dv = 4 * g + e, i = iw + r;
         Vt[dv * LDT + i] = Ub[bf][i * kScanRows + dv] - acc[e];
       }
     }
-    __syncthreads();  // V'ᵀ complete; every read of S for V' done
-    if (wave == 4) {
+    __syncthreads();  // V'ᵀ complete; every read of S for V' and X done
+    if (wave >= 4) {  // O[i][dv] = γ_i X[i][dv] + Σ_{j ≤ i} M[i][j] V'ᵀ[dv][j]
+      f4 vb[4];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {  // V'ᵀ, for `out`
-        const int idx = 64 * n + lane, row = idx >> 4, c4 = idx & 15;
-        *(f4*)(io + kOffVt + (dv0 + row) * C + 4 * c4) = *(const f4*)(Vt + row * LDT + 4 * c4);
+      for (int jb = 0; jb < 4; ++jb) vb[jb] = *(const f4*)(Vt + r * LDT + 16 * jb + 4 * g);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        if (jb <= ow) {
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) x = mfma4(ma[jb][s4], vb[jb][s4], x);
+        }
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next chunk's tiles have landed
-      if (lane == 0 && c + 1 < nch) Gc[bf ^ 1] = gc_next;
+      // the next chunk's tiles and operands have landed (issued a phase ago); the stores below stay in flight
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const uint32_t tb = c * C + i0 + 4 * g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (tb + e < T) o[((size_t)(tb + e) * NV + h) * DV + dv0 + r] = x[e];
+      take_ops();
+      if (wave == 4 && lane == 0 && c + 1 < nch) Gc[bf ^ 1] = gc_next;
     } else {  // S[dv][d] ← γ_C S[dv][d] + Σ_j V'ᵀ[dv][j] K̃ᵀ[d][j]; each wave reads and writes only its own columns
       const float gC = Gc[bf];
 #pragma unroll
@@ -487,80 +540,6 @@ __global__ __launch_bounds__(320) void delta_chunk_scan_kernel(float* __restrict
   }
 }
 
-// ---------------------------------------------------------------------------
-// out: one workgroup per (chunk, value head, 32 value columns):
-//   O[i][dv] = γ_i Σ_d Q[i][d] S[dv][d] + Σ_{j ≤ i} M[i][j] V'ᵀ[dv][j]
-// Wave w owns tokens 16 w .. + 16 and loads its own operand rows (Q and M)
-// straight into registers in the MFMA's k layout; only the shared S and V'
-// columns go through LDS (26 KB), so several workgroups share a CU. M is
-// lower triangular: wave w sums token blocks jb ≤ w only.
-constexpr int kOutCols = 32;
-
-__global__ __launch_bounds__(256) void delta_chunk_out_kernel(const float* __restrict__ q,
-                                                              const float* __restrict__ ws, float* __restrict__ o,
-                                                              uint32_t T) {
-  __shared__ __attribute__((aligned(16))) float Sq[kOutCols * LDF];
-  __shared__ __attribute__((aligned(16))) float Vq[kOutCols * LDT];
-  const uint32_t c = blockIdx.x, h = blockIdx.y, hk = h >> 1, dv0 = blockIdx.z * kOutCols, t0 = c * C;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  const int i0 = 16 * wave;
-  const float* in = ws + ((size_t)c * NV + h) * kWsStride;
-  // this wave's operands: Q[i0 + r][32 g .. + 32] and M[i0 + r][16 jb + 4 g .. + 4], γ of its rows
-  f4 qa[8], ma[4];
-  {
-    const uint32_t t = t0 + i0 + r;
-    const float* qr = q + ((size_t)min(t, T - 1) * NK + hk) * DK + 32 * g;  // rows past T: any finite row
-#pragma unroll
-    for (int n = 0; n < 8; ++n) qa[n] = *(const f4*)(qr + 4 * n);
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-      ma[jb] = jb <= wave ? *(const f4*)(in + kOffM + (i0 + r) * C + 16 * jb + 4 * g) : f4{0.f, 0.f, 0.f, 0.f};
-  }
-  f4 gi;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) gi[e] = in[kOffGam + i0 + 4 * g + e];
-#pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    const int e = (tid + 256 * n) * 4;
-    *(f4*)(Sq + (e >> 7) * LDF + (e & 127)) = *(const f4*)(in + kOffS + (dv0 + (e >> 7)) * DK + (e & 127));
-  }
-#pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const int e = (tid + 256 * n) * 4;
-    *(f4*)(Vq + (e >> 6) * LDT + (e & 63)) = *(const f4*)(in + kOffVt + (dv0 + (e >> 6)) * C + (e & 63));
-  }
-  __syncthreads();
-#pragma unroll
-  for (int dt = 0; dt < kOutCols / 16; ++dt) {
-    f4 sb[8], vb[4];
-    const float* sr = Sq + (16 * dt + r) * LDF + 32 * g;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) sb[n] = *(const f4*)(sr + 4 * n);
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) vb[jb] = *(const f4*)(Vq + (16 * dt + r) * LDT + 16 * jb + 4 * g);
-    __builtin_amdgcn_sched_barrier(0);
-    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = mfma4(qa[n][e], sb[n][e], acc);
-    acc *= gi;
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      if (jb <= wave) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = mfma4(ma[jb][s], vb[jb][s], acc);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t t = t0 + i0 + 4 * g + e;
-      if (t < T) o[((size_t)t * NV + h) * DV + dv0 + 16 * dt + r] = acc[e];
-    }
-  }
-}
-
 size_t delta_chunk_ws_floats(uint32_t t) { return (size_t)((t + C - 1) / C) * NV * kWsStride; }
 
 hipError_t launch_gated_delta_chunked(const float* q, const float* k, const float* v, const float* a, const float* b,
@@ -570,9 +549,8 @@ hipError_t launch_gated_delta_chunked(const float* q, const float* k, const floa
   const uint32_t nch = (t + C - 1) / C;
   hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(nch, NV), dim3(256), 0, s, q, k, v, a, b, ldab, a_log, dt_bias, ws,
                      t);
-  hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(320), 0, s, ws, state_in, state_out, t,
-                     write_state ? 1u : 0u);
-  hipLaunchKernelGGL(delta_chunk_out_kernel, dim3(nch, NV, DV / kOutCols), dim3(256), 0, s, q, ws, o, t);
+  hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(512), 0, s, ws, q, state_in, state_out, o,
+                     t, write_state ? 1u : 0u);
   return hipGetLastError();
 }
 
