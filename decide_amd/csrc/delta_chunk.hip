@@ -378,6 +378,38 @@ __device__ __forceinline__ f4 nt_tile_swz(const float* A, int lda, const float* 
   return acc + acc2;
 }
 
+// Two tiles that share A: acc0 += Σ_k A[r][k] B[b0 + r][k] and acc1 the same
+// with rows b1 of B, in nt_tile_swz's order per tile (two chains each, summed
+// at the end) but with one read of A and the four chains interleaved.
+template <int KLEN, int CH>
+__device__ __forceinline__ void nt_tile2_swz(const float* A, int lda, const float* B, int b0, int b1, int r, int g,
+                                             f4& acc0, f4& acc1) {
+  constexpr int P = KLEN / 4, Q = P / 4;
+  f4 a[Q], u[Q], w[Q];
+  const float* pa = A + r * lda + g * P;
+  const float* pu = B + (b0 + r) * CH * 4;
+  const float* pw = B + (b1 + r) * CH * 4;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    a[q] = *(const f4*)(pa + 4 * q);
+    u[q] = *(const f4*)(pu + 4 * ((g * Q + q) ^ r));
+    w[q] = *(const f4*)(pw + 4 * ((g * Q + q) ^ r));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  f4 acc0b = f4{0.f, 0.f, 0.f, 0.f}, acc1b = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      acc0 = mfma4(a[q][e], u[q][e], acc0);
+      acc1 = mfma4(a[q][e], w[q][e], acc1);
+      acc0b = mfma4(a[q][e + 1], u[q][e + 1], acc0b);
+      acc1b = mfma4(a[q][e + 1], w[q][e + 1], acc1b);
+    }
+  acc0 += acc0b;
+  acc1 += acc1b;
+}
+
 __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict__ ws, const float* __restrict__ q,
                                                                const float* state_in, float* state_out,
                                                                float* __restrict__ o, uint32_t T,
@@ -519,15 +551,18 @@ __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict
       if (wave == 4 && lane == 0 && c + 1 < nch) Gc[bf ^ 1] = gc_next;
     } else {  // S[dv][d] ← γ_C S[dv][d] + Σ_j V'ᵀ[dv][j] K̃ᵀ[d][j]; each wave reads and writes only its own columns
       const float gC = Gc[bf];
+      const int d0 = 32 * wave;
+      f4 acc0, acc1;
 #pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        const int d0 = 16 * (2 * wave + q2);
-        f4 acc;
+      for (int e = 0; e < 4; ++e) {
+        acc0[e] = gC * Ss[(4 * g + e) * LDF + d0 + r];
+        acc1[e] = gC * Ss[(4 * g + e) * LDF + d0 + 16 + r];
+      }
+      nt_tile2_swz<C, 16>(Vt, LDT, Kb[bf], d0, d0 + 16, r, g, acc0, acc1);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = gC * Ss[(4 * g + e) * LDF + d0 + r];
-        acc = nt_tile_swz<C, 16>(Vt, LDT, Kb[bf], d0, r, g, acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) Ss[(4 * g + e) * LDF + d0 + r] = acc[e];
+      for (int e = 0; e < 4; ++e) {
+        Ss[(4 * g + e) * LDF + d0 + r] = acc0[e];
+        Ss[(4 * g + e) * LDF + d0 + 16 + r] = acc1[e];
       }
     }
     __syncthreads();  // S and the next chunk's tiles are in place
