@@ -11,8 +11,9 @@
 //     bytes per row per instruction, which is the B operand of
 //     v_mfma_f32_16x16x32_f16 as it stands. X rows (clamped to M − 1) come
 //     from L2 the same way as the A operand.
-//   * Loads run D k blocks ahead through a register ring, with exact vmcnt
-//     waits (inline asm, in program order).
+//   * Loads run D k blocks ahead through a register ring. They are plain
+//     vector loads, so the compiler sees every one and places the waits
+//     before each register's first use itself.
 //   * The 4 waves' partial sums meet in LDS and are added in wave order;
 //     split-K across workgroups writes fp32 partials that
 //     splitk_reduce_kernel sums in split order. Deterministic.
@@ -28,7 +29,6 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSK = 128;  // k per block
 constexpr int kD = 3;     // k blocks in flight per wave
-constexpr int kLoads = 12;  // load instructions per k block: 4 for X, 8 for the two W fragments
 
 template <int B, int E, typename Fn>
 __device__ __forceinline__ void sfor(Fn&& fn) {
@@ -38,16 +38,7 @@ __device__ __forceinline__ void sfor(Fn&& fn) {
   }
 }
 
-__device__ __forceinline__ void load16(h8& dst, const _Float16* src) {
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(src) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ void tie(h8& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void load16(h8& dst, const _Float16* src) { dst = *(const h8*)src; }
 
 __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -93,9 +84,6 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(const TileArgs a) {
     constexpr int s = decltype(slot)::value;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      tie(xs[s][q]);
-      tie(ws0[s][q]);
-      tie(ws1[s][q]);
       acc0 = mfma16(xs[s][q], ws0[s][q], acc0);
       acc1 = mfma16(xs[s][q], ws1[s][q], acc1);
     }
@@ -107,15 +95,10 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(const TileArgs a) {
   for (; i + kD <= nbw; i += kD) {
     sfor<0, kD>([&](auto sc) {
       constexpr int s = decltype(sc)::value;
-      if (i + s + kD <= nbw)
-        wait_vm<(kD - 1) * kLoads>();  // blocks i + s + 1 .. i + s + kD − 1 may still be in flight
-      else
-        wait_vm<0>();
       comp(sc);
       if (i + s + kD < nbw) load(sc, i + s + kD);
     });
   }
-  wait_vm<0>();
   sfor<0, kD>([&](auto sc) {
     if (i + decltype(sc)::value < nbw) comp(sc);
   });
