@@ -13,7 +13,9 @@
 // and, for every chunk independently once its S and V' are known,
 //   O = diag(γ) Q Sᵀ + M V'.
 // Two kernels:
-//   prep: W, U, M and K̃ᵀ = (diag(γ_C/γ) K)ᵀ for every (chunk, value head);
+//   prep: W, U, M and K̃ᵀ = (diag(γ_C/γ) K)ᵀ for every (chunk, value head),
+//         one workgroup per (chunk, key head) for the Gram tiles the key
+//         head's two value heads share;
 //   scan: the chunks in order for each (head, 16 value rows), keeping the
 //         state slice in LDS, and O for those rows from each chunk's
 //         starting S and V' while the next state is being formed.
@@ -111,36 +113,41 @@ __device__ __forceinline__ void lower_block(int p, int& i, int& j) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// prep: one workgroup per (chunk, value head).
-__global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
+// prep: one workgroup per (chunk, key head). The Gram tiles Q Kᵀ and K Kᵀ are
+// the key head's, shared by its two value heads 2 hk and 2 hk + 1 (which
+// differ only in their gates), so they are computed once and scaled for each;
+// then waves 4 hh .. 4 hh + 3 do value head 2 hk + hh's inversion, W and U.
+__global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                                const float* __restrict__ v, const float* __restrict__ a,
                                                                const float* __restrict__ b, uint32_t ldab,
                                                                const float* __restrict__ a_log,
                                                                const float* __restrict__ dt_bias, float* __restrict__ ws,
                                                                uint32_t T) {
-  // 74 KB of LDS, so two workgroups share a CU: Q is staged only for M = Q Kᵀ, and A and T then take its
-  // place; V never goes through LDS (each wave loads its U operand into registers during the inversion).
-  constexpr int kR2 = C * LDF > 2 * C * LDT ? C * LDF : 2 * C * LDT;
+  // 112 KB of LDS, one workgroup of 8 waves per CU: Q is staged only for the Gram tiles, whose results wait in
+  // registers until every wave is past them; then each value head's A and T take Q's place. V never goes
+  // through LDS (each wave loads its U operand into registers during the inversion).
+  constexpr int kAT = C * LDT;  // one [64][68] tile
+  constexpr int kR2 = C * LDF > 4 * kAT ? C * LDF : 4 * kAT;
   __shared__ __attribute__((aligned(16))) float Ks[C * LDF];
-  __shared__ __attribute__((aligned(16))) float R2[kR2];  // Q; then A | T
-  __shared__ __attribute__((aligned(16))) float Lg[C], Bt[C], Gm[C], SCw[C], Rh[C];
-  __shared__ float Ysc[4 * 16 * 17];  // per-wave 16 × 16 scratch of the blocked inversion
-  float* const Qs = R2;
-  float* const As = R2;
-  float* const Ts = R2 + C * LDT;
-  const uint32_t c = blockIdx.x, h = blockIdx.y, hk = h >> 1, t0 = c * C;
+  __shared__ __attribute__((aligned(16))) float R2[kR2];  // Q; then A0 | T0 | A1 | T1
+  __shared__ __attribute__((aligned(16))) float Lg[2][C], Bt[2][C], Gm[2][C], SCw[2][C], Rh[2][C];
+  __shared__ float Ysc[8 * 16 * 17];  // per-wave 16 × 16 scratch of the blocked inversion
+  const uint32_t c = blockIdx.x, hk = blockIdx.y, t0 = c * C;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
-  float* out = ws + ((size_t)c * NV + h) * kWsStride;
+  const int hh = wave >> 2, lw = wave & 3;  // this wave's value head (of the key head's two), and its wave in that half
+  const uint32_t h = 2 * hk + hh;
+  float* const As = R2 + 2 * hh * kAT;
+  float* const Ts = As + kAT;
+  float* const out0 = ws + ((size_t)c * NV + 2 * hk) * kWsStride;
+  float* const out = out0 + hh * kWsStride;
 
-  {  // all loads in flight before the first LDS store
-    f4 xk[8], xq[8];
-    fetch_rows(xk, k, t0, T, NK, hk, tid);
-    fetch_rows(xq, q, t0, T, NK, hk, tid);
-    stage_rows(Ks, xk, tid);
-    stage_rows(Qs, xq, tid);
+  {  // threads 0-255 stage K, 256-511 Q; all loads in flight before the first LDS store
+    f4 x[8];
+    fetch_rows(x, tid < 256 ? k : q, t0, T, NK, hk, tid & 255);
+    stage_rows(tid < 256 ? Ks : R2, x, tid & 255);
   }
-  if (wave == 0) {
+  if (lw == 0) {  // waves 0 and 4: value head h's gates
     const uint32_t t = t0 + lane;
     float lam = 0.f, bt = 0.f;
     if (t < T) {
@@ -154,48 +161,68 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
     }
     const float last = __shfl(lam, 63, 64);
     const float gm = expf(lam);
-    Lg[lane] = lam;
-    Bt[lane] = bt;
-    Gm[lane] = gm;
-    SCw[lane] = bt * gm;
-    Rh[lane] = expf(last - lam);
+    Lg[hh][lane] = lam;
+    Bt[hh][lane] = bt;
+    Gm[hh][lane] = gm;
+    SCw[hh][lane] = bt * gm;
+    Rh[hh][lane] = expf(last - lam);
   }
   __syncthreads();
 
-  // Q Kᵀ → M (lower incl. diagonal, γ_i/γ_j), then K Kᵀ → A (strictly lower, β_i γ_i/γ_j) over Q's LDS: the
-  // 10 blocks on or below the diagonal of each; M's blocks above it are written as zeros, A's are never read
-  for (int tt = wave; tt < 20; tt += 4) {
-    const bool isq = tt < 10;
-    if (tt >= 10 && tt - 4 < 10) __syncthreads();  // every wave is past its last M block: Q is dead
-    int ti, tj;
-    lower_block(isq ? tt : tt - 10, ti, tj);
-    const f4 acc = nt_tile<DK>((isq ? Qs : Ks) + 16 * ti * LDF, LDF, Ks + 16 * tj * LDF, LDF, r, g,
-                               f4{0.f, 0.f, 0.f, 0.f});
-    const int j = 16 * tj + r;
+  // The 20 Gram tiles: tile t < 10 is block t of Q Kᵀ (lower triangle incl. diagonal), t ≥ 10 block t − 10 of
+  // K Kᵀ (strictly lower); wave w takes t = w, w + 8, w + 16. Each tile then gives both value heads' M
+  // (γ_i/γ_j, to global; blocks above the diagonal written as zeros) or A (β_i γ_i/γ_j, over Q's LDS).
+  f4 gacc[3];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * ti + 4 * g + e;
-      const float rr = i >= j ? expf(Lg[i] - Lg[j]) : 0.f;
-      if (!isq)
-        As[i * LDT + j] = i > j ? Bt[i] * rr * acc[e] : 0.f;
-      else
-        out[kOffM + i * C + j] = rr * acc[e];
+  for (int u = 0; u < 3; ++u) {
+    const int tt = wave + 8 * u;
+    if (tt < 20) {
+      int ti, tj;
+      lower_block(tt < 10 ? tt : tt - 10, ti, tj);
+      gacc[u] = nt_tile<DK>((tt < 10 ? R2 : Ks) + 16 * ti * LDF, LDF, Ks + 16 * tj * LDF, LDF, r, g,
+                            f4{0.f, 0.f, 0.f, 0.f});
     }
   }
-  for (int e = tid; e < C * C; e += 256)
-    if ((e & 63) >> 4 > e >> 10) out[kOffM + e] = 0.f;
-  // K̃ᵀ[d][j] = (γ_C/γ_j) K[j][d] for the scan
+  __syncthreads();  // every wave is past its Gram tiles: Q is dead
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    const int e = tid + 256 * n, d = e >> 4, j4 = (e & 15) * 4;
-    f4 x;
+  for (int u = 0; u < 3; ++u) {
+    const int tt = wave + 8 * u;
+    if (tt < 20) {
+      const bool isq = tt < 10;
+      int ti, tj;
+      lower_block(isq ? tt : tt - 10, ti, tj);
+      const int j = 16 * tj + r;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = Rh[j4 + u] * Ks[(j4 + u) * LDF + d];
-    *(f4*)(out + kOffKt + d * C + j4) = x;
+      for (int vh = 0; vh < 2; ++vh)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * ti + 4 * g + e;
+          const float rr = i >= j ? expf(Lg[vh][i] - Lg[vh][j]) : 0.f;
+          if (!isq)
+            R2[2 * vh * kAT + i * LDT + j] = i > j ? Bt[vh][i] * rr * gacc[u][e] : 0.f;
+          else
+            out0[vh * kWsStride + kOffM + i * C + j] = rr * gacc[u][e];
+        }
+    }
   }
-  if (tid < C) out[kOffGam + tid] = Gm[tid];
+  for (int e = tid; e < 2 * C * C; e += 512) {
+    const int f = e & (C * C - 1);
+    if ((f & 63) >> 4 > f >> 10) out0[(e >> 12) * kWsStride + kOffM + f] = 0.f;
+  }
+  {  // K̃ᵀ[d][j] = (γ_C/γ_j) K[j][d] for the scan; threads 0-255 for value head 2 hk, 256-511 for 2 hk + 1
+    const int vh = tid >> 8, t8 = tid & 255;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int e = t8 + 256 * n, d = e >> 4, j4 = (e & 15) * 4;
+      f4 x;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = Rh[vh][j4 + u] * Ks[(j4 + u) * LDF + d];
+      *(f4*)(out0 + vh * kWsStride + kOffKt + d * C + j4) = x;
+    }
+  }
+  if (tid < 2 * C) out0[(tid >> 6) * kWsStride + kOffGam + (tid & 63)] = Gm[tid >> 6][tid & 63];
 
-  // This wave's U operand, V[t0 + 16 jb + 4 g + s][16 (2 wave + q2) + r], straight into registers; the loads
+  // This wave's U operand, V[t0 + 16 jb + 4 g + s][16 (2 lw + q2) + r], straight into registers; the loads
   // run during the inversion below.
   f4 vr[2][4];
 #pragma unroll
@@ -205,18 +232,18 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const uint32_t t = t0 + 16 * jb + 4 * g + s4;
-        vr[q2][jb][s4] = t < T ? v[((size_t)t * NV + h) * DV + 16 * (2 * wave + q2) + r] : 0.f;
+        vr[q2][jb][s4] = t < T ? v[((size_t)t * NV + h) * DV + 16 * (2 * lw + q2) + r] : 0.f;
       }
 
-  // T = (I + A)⁻¹, blocked 4 × 4 over 16 × 16 blocks. Diagonal blocks by forward
-  // substitution (wave w, lane j < 16 owns column j of block w); then the
-  // blocks below the diagonal, one block-diagonal at a time,
+  // T = (I + A)⁻¹ per value head, blocked 4 × 4 over 16 × 16 blocks. Diagonal blocks by forward
+  // substitution (wave lw of the head's half, lane j < 16 owns column j of block lw); then the blocks below
+  // the diagonal, one block-diagonal at a time,
   //   T_ij = −T_ii Σ_{k=j}^{i−1} A_ik T_kj,
   // as 16 × 16 MFMA products through a per-wave LDS scratch block.
-  for (int e = tid; e < C * LDT; e += 256) Ts[e] = 0.f;
+  for (int e = tid; e < 2 * kAT; e += 512) R2[(2 * (e / kAT) + 1) * kAT + e % kAT] = 0.f;
   __syncthreads();
   {
-    const int jb = wave;
+    const int jb = lw;
     if (lane < 16) {
       float x[16];
       sfor<0, 16>([&](auto ic) {
@@ -236,8 +263,8 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
   }
   __syncthreads();
   for (int d = 1; d < 4; ++d) {
-    if (wave < 4 - d) {
-      const int j = wave, i = wave + d;
+    if (lw < 4 - d) {
+      const int j = lw, i = lw + d;
       f4 y = f4{0.f, 0.f, 0.f, 0.f};
       for (int kb = j; kb < i; ++kb) {  // Y = Σ_k A_ik T_kj
 #pragma unroll
@@ -257,17 +284,17 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(const float* __re
     __syncthreads();
   }
 
-  // W = T diag(βγ) K and U = T diag(β) V. Wave w: key/value columns 16 td for td = 2w, 2w + 1. T is lower
-  // triangular, so row block ti sums over token blocks jb ≤ ti; within a block lane group g holds tokens
-  // 16 jb + 4 g .. + 4 (one ds_read_b128 of T and of the scale), and the B operand K[j][16 td + r] is
-  // conflict-free with the row stride of 132 floats (V's comes from registers).
+  // W = T diag(βγ) K and U = T diag(β) V. Wave lw of the head's half: key/value columns 16 td for td = 2 lw,
+  // 2 lw + 1. T is lower triangular, so row block ti sums over token blocks jb ≤ ti; within a block lane
+  // group g holds tokens 16 jb + 4 g .. + 4 (one ds_read_b128 of T and of the scale), and the B operand
+  // K[j][16 td + r] is conflict-free with the row stride of 132 floats (V's comes from registers).
 #pragma unroll
   for (int isu = 0; isu < 2; ++isu) {
-    const float* sc = isu ? Bt : SCw;
+    const float* sc = isu ? Bt[hh] : SCw[hh];
     float* dst = out + (isu ? kOffU : kOffW);
 #pragma unroll
     for (int q2 = 0; q2 < 2; ++q2) {
-      const int d0 = 16 * (2 * wave + q2);
+      const int d0 = 16 * (2 * lw + q2);
       sfor<0, 4>([&](auto tic) {
         constexpr int ti = decltype(tic)::value;
         f4 ta[ti + 1], sv[ti + 1], rb[ti + 1];
@@ -582,7 +609,7 @@ hipError_t launch_gated_delta_chunked(const float* q, const float* k, const floa
                                       float* state_out, float* o, float* ws, uint32_t t, uint32_t ldab,
                                       bool write_state, hipStream_t s) {
   const uint32_t nch = (t + C - 1) / C;
-  hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(nch, NV), dim3(256), 0, s, q, k, v, a, b, ldab, a_log, dt_bias, ws,
+  hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(nch, NK), dim3(512), 0, s, q, k, v, a, b, ldab, a_log, dt_bias, ws,
                      t);
   hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(512), 0, s, ws, q, state_in, state_out, o,
                      t, write_state ? 1u : 0u);
