@@ -101,6 +101,30 @@ def test_gated_delta_matches_oracle(gpu, kernels_delta_sequential, kernels_delta
 
 
 @pytest.mark.parametrize("impl", ["chunked", "sequential"])
+def test_gated_delta_unit_gate_known_answer(gpu, kernels_delta_sequential, kernels_delta_chunked, stream, impl):
+    """decide's known answer (cpu_ref.rs:224-236) through both GPU implementations: one step, beta = 1 (b = 50),
+    g = 1 (A_log = -inf), k = q = e_0 and v = 3 e_5 in head 0: o = v and S = v kᵀ exactly, all else zero."""
+    kernels = kernels_delta_chunked if impl == "chunked" else kernels_delta_sequential
+    t = 1
+    q = np.zeros((t, NK, DK), np.float32)
+    q[0, 0, 0] = 1.0
+    k = q.copy()
+    v = np.zeros((t, NV, DV), np.float32)
+    v[0, 0, 5] = 3.0
+    p = np.zeros((t, LIN_IN_N), np.float32)
+    p[:, LIN_B:LIN_B + NV] = 50.0
+    a_log = np.full(NV, -np.inf, np.float32)
+    o, s1 = _run_delta(kernels, stream, q, k, v, p, a_log, np.zeros(NV, np.float32),
+                       np.zeros((NV, DV, DK), np.float32), t)
+    want_o = np.zeros_like(o)
+    want_o[0, 0, 5] = 3.0
+    want_s = np.zeros_like(s1)
+    want_s[0, 5, 0] = 3.0
+    np.testing.assert_array_equal(o, want_o)
+    np.testing.assert_array_equal(s1, want_s)
+
+
+@pytest.mark.parametrize("impl", ["chunked", "sequential"])
 def test_gated_delta_renormalises_a_fast_decay(gpu, kernels_delta_sequential, kernels_delta_chunked, stream, impl):
     """g ≈ e^-37 per token: the sequential kernel's running scale drops below 2^-60 within two tokens,
     the chunked kernel's within-chunk ratios γ_i/γ_j underflow to 0."""

@@ -102,6 +102,25 @@ def test_delta_one_token_from_zero_state_closed_form():
         np.testing.assert_allclose(s1[h], beta * np.outer(v[0, h], k[0, hk]), rtol=1e-5, atol=1e-8)
 
 
+def test_delta_rule_with_unit_gate_is_a_delta_update():
+    """decide's own known answer (cpu_ref.rs:224-236): one step with beta = 1 (b = 50) and g = 1 (A_log = -inf,
+    so exp(A_log) = 0): S = v kᵀ with k = e_0, so o = S q = v; every other value stays zero."""
+    t = 1
+    q = np.zeros((t, NK, DK), np.float32)
+    q[0, 0, 0] = 1.0
+    k = q.copy()
+    v = np.zeros((t, NV, DV), np.float32)
+    v[0, 0, 5] = 3.0  # head 0, column 5
+    a, b = np.zeros((t, NV), np.float32), np.full((t, NV), 50.0, np.float32)
+    st = np.zeros((NV, DV, DK), np.float32)
+    o, s1 = orc.gated_delta(q, k, v, a, b, np.full(NV, -np.inf, np.float32), np.zeros(NV, np.float32), st, t)
+    assert abs(o[0, 0, 5] - 3.0) < 1e-5
+    assert abs(s1[0, 5, 0] - 3.0) < 1e-5  # state[5 * DK]: head 0, value row 5, key column 0
+    o[0, 0, 5] = 0.0
+    s1[0, 5, 0] = 0.0
+    assert not o.any() and not s1.any()
+
+
 def test_delta_without_writes_only_decays_the_state():
     t = 4
     q, k, v, a, b, a_log, dt_bias, st = _delta_inputs(t, 30, state_std=0.3)
