@@ -274,7 +274,12 @@ int dh_kv_norm_rope(dh_ctx* ctx, void* stream, const float* pkv, const float* kw
  * read from pq (fp32, row stride ldq) at column 4096 + 256 h + d. y fp16
  * [rows, 4096] = softmax(q·kᵀ/16)·v ⊙ σ(gate). rows >= 1, ldq >= 8192 and even;
  * q, kc, vc 16-byte, pq 8-byte, qpos and y 4-byte aligned. Cache rows
- * 0..=max(qpos) must hold finite values. */
+ * 0..=max(qpos) must hold finite values. Long query blocks' keys are split
+ * across workgroups (cut points at fixed key offsets, sized as if the rows sat
+ * at positions 0..rows-1) and merged through the context's forward-kernel
+ * workspace, which dh_warm_up sizes. The cut length depends only on `rows`:
+ * a row's bits depend on its own query, position and cache rows, and, when its
+ * keys span a cut, on the call's row count (rounding only). */
 int dh_attention(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const float* pq,
                  const uint32_t* qpos, uint16_t* y, uint32_t rows, uint32_t ldq);
 
