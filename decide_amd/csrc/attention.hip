@@ -16,8 +16,9 @@
 //     ONE query row for keys {4g..4g+3, 16+4g..16+4g+3} (g = lane / 16), which
 //     is exactly the B operand Pᵀ needs if the 32 keys of a block are taken
 //     in that order — so P goes from scores to MFMA operand without leaving
-//     registers. Vᵀ is staged key-contiguous (transposed on the way into LDS)
-//     and read in the same key order.
+//     registers. Vᵀ is transposed on the way into LDS with its keys in that
+//     same order, so each lane reads its 8 keys of a Vᵀ row with one
+//     16-byte LDS read.
 //   * Online softmax in the exp2 domain; a row's max is reduced across the
 //     four lane groups that hold it; the running sum stays
 //     per lane and is reduced once at the end (both reductions by cross-row
@@ -56,7 +57,8 @@ constexpr int kHD = 256, kNQ = 16, kQDim = kNQ * kHD;
 constexpr int kBQ = 32;    // query rows per workgroup (2 blocks of 16)
 constexpr int kBKey = 32;  // keys per block
 constexpr int kKLD = kHD + 8;  // K tile row stride (halves): 528 B, conflict-free 16-lane reads
-constexpr int kVLD = kBKey + 4;  // Vᵀ tile row stride (halves): 72 B = 18 banks, so 16 rows hit distinct bank pairs
+// Vᵀ tile row stride (halves): 80 B = 20 banks, 16-byte aligned, so 16 rows' ds_read_b128 hit distinct bank quads
+constexpr int kVLD = kBKey + 8;
 constexpr float kScaleLog2 = 0.0625f * 1.4426950408889634f;  // 1/16 · log2(e)
 constexpr float kNeg = -1e30f;
 constexpr float kLazy = 8.0f;  // log2 headroom of the softmax reference point (weights up to 256)
@@ -152,6 +154,9 @@ __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restri
   // staging: K rows as 16-byte chunks (thread → key id / 32, chunk id % 32, two per thread);
   // V as key pairs × 8-dim chunks, transposed into vts on the way in
   const int kp = tid & 15, dc = tid >> 4;
+  // Vᵀ keys are stored in the order the P operand takes them: lane group g's keys {4g..4g+3, 16+4g..16+4g+3} at
+  // 8g .. 8g+7, so each lane reads its 8 keys with one ds_read_b128. Key pair (2 kp, 2 kp + 1) lands at vpos.
+  const int vpos = ((kp >> 1 & 3) << 3) + ((kp >> 3) << 2) + ((kp & 1) << 1);
   // two register slots of staged rows: block b + 2 is fetched while block b computes, so a fetch has two
   // blocks' work to land (one block's was not enough: the L2 round trip outlasts it)
   h8 kpre[2][2], vpre[2][2];
@@ -174,7 +179,7 @@ __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restri
       *(h8*)(ks + key * kKLD + 8 * c16) = kpre[sl][i];
     }
 #pragma unroll
-    for (int d = 0; d < 8; ++d) *(h2*)(vts + (8 * dc + d) * kVLD + 2 * kp) = h2{vpre[sl][0][d], vpre[sl][1][d]};
+    for (int d = 0; d < 8; ++d) *(h2*)(vts + (8 * dc + d) * kVLD + vpos) = h2{vpre[sl][0][d], vpre[sl][1][d]};
     __syncthreads();
     fetch(kb0 + 2 * kBKey, sc);  // in flight during this block and the next (rows past kmax are clamped reads)
 
@@ -223,9 +228,7 @@ __global__ __launch_bounds__(512) void attention_kernel(const _Float16* __restri
     lsum += ps;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) {
-      const _Float16* vr = vts + (16 * dt + rl) * kVLD + 4 * g;
-      const h4 lo = *(const h4*)vr, hi = *(const h4*)(vr + 16);
-      const h8 va = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const h8 va = *(const h8*)(vts + (16 * dt + rl) * kVLD + 8 * g);
       oacc[dt] = mfma16(va, pb, oacc[dt]);
     }
   };
