@@ -325,19 +325,23 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const float* __re
 // ---------------------------------------------------------------------------
 // scan: one workgroup per (value head, 16 value rows); the 8 workgroups of a
 // head have ids 32 apart, so they run on one XCD and share its L2 for the
-// per-chunk matrices. Waves 0-3 carry the recurrence and touch LDS only;
-// waves 4-7 ("out waves", one per 16 tokens of the chunk) do all the global
-// memory work and the chunk's output, so their stalls never hold up the
-// recurrence's MFMAs:
-//   chunk c, waves 0-3:  V'ᵀ = Uᵀ − S Wᵀ (wave w: tokens 16 w .. + 16)
+// per-chunk matrices. Waves 0-3 carry the recurrence and touch global memory
+// only to DMA the next chunk's tiles where they would otherwise wait at a
+// barrier; waves 4-7 ("out waves", one per 16 tokens of the chunk) form the
+// chunk's output:
+//   chunk c, waves 0-3:  V'ᵀ = Uᵀ − S Wᵀ (wave w: tokens 16 w .. + 16); DMA
+//                        a quarter of chunk c + 1's W and U slice into the
+//                        other LDS buffer
 //                        | barrier |
-//                        S = γ_C S + V'ᵀ K̃ (wave w: key columns 32 w .. + 32)
-//   chunk c, waves 4-7:  DMA a quarter of chunk c + 1's W, K̃ᵀ and U slice
-//                        into the other LDS buffer; X = Q Sᵀ for their
-//                        tokens (S is still the chunk's starting state)
+//                        S = γ_C S + V'ᵀ K̃ (wave w: key columns 32 w .. + 32);
+//                        DMA a quarter of chunk c + 1's K̃ᵀ; wait for the W
+//                        and U DMAs
+//   chunk c, waves 4-7:  X = Q Sᵀ for their tokens (S is still the chunk's
+//                        starting state), loading chunk c + 1's Q rows
+//                        between the products
 //                        | barrier |
-//                        O = diag(γ) X + M V' (V' complete), stored; wait
-//                        for the DMA
+//                        O = diag(γ) X + M V' (V' complete), loading chunk
+//                        c + 1's M rows and γ first; stored
 //   | barrier |
 // W and K̃ᵀ land by global→LDS DMA (16 bytes per lane, 1 KB per instruction)
 // in an unpadded layout whose 16-byte chunks are XOR-swizzled by row
@@ -454,67 +458,115 @@ __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict
   const uint32_t nch = (T + C - 1) / C;
   auto slot = [&](uint32_t c) { return ws + ((size_t)c * NV + h) * kWsStride; };
 
-  // out wave ow's quarter of chunk c's W, K̃ᵀ and U slice into buffer bf by DMA
-  auto dma_chunk = [&](uint32_t c, int bf, int ow) {
-    const float* in = slot(c);
-    const uint64_t bw = sgpr_ptr(in + kOffW), bk = sgpr_ptr(in + kOffKt), bu = sgpr_ptr(in + kOffU);
-    const uint32_t wl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Wb[bf]);
-    const uint32_t kl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Kb[bf]);
-    const uint32_t ul = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Ub[bf]);
-    const int n0 = 8 * ow;
-    // W: LDS chunk 64 n + lane = row 2 n + lane / 32, slot lane % 32
-    auto dma_w = [&](int n) {
-      const int row = 2 * n + (lane >> 5), c4 = (lane & 31) ^ (row & 15);
-      return (uint32_t)((row * DK + 4 * c4) * 4);
-    };
-    dma16_lds<true>(wl + n0 * 1024, dma_w(n0), bw);
-#pragma unroll
-    for (int n = 1; n < 8; ++n) dma16_lds(wl + (n0 + n) * 1024, dma_w(n0 + n), bw);
-    // K̃ᵀ: row 4 n + lane / 16, slot lane % 16
-    auto dma_k = [&](int n) {
-      const int row = 4 * n + (lane >> 4), c4 = (lane & 15) ^ (row & 15);
-      return (uint32_t)((row * C + 4 * c4) * 4);
-    };
-#pragma unroll
-    for (int n = 0; n < 8; ++n) dma16_lds(kl + (n0 + n) * 1024, dma_k(n0 + n), bk);
-    // U rows, columns dv0 .. + 16: row 16 n + lane / 4, chunk lane % 4
-    dma16_lds(ul + ow * 1024, (uint32_t)(((16 * ow + (lane >> 2)) * DK + dv0 + 4 * (lane & 3)) * 4), bu);
+  // The next chunk's operands are loaded during this one: W, K̃ᵀ and the U slice by DMA into buffer bf ^ 1, each
+  // recurrence wave its quarter, issued where that wave would otherwise wait at a barrier (W and U after its V'
+  // products, K̃ᵀ after its state update: each has the following phase to land); Q, M and γ rows into the out
+  // waves' registers, spread over their products. The vector memory unit passes about one 1 KB instruction per
+  // 30 clocks for the whole CU, and a wave stalls at each instruction it cannot hand over: issued back to back
+  // by the out waves, the chunk's 114 instructions held them (and through the barriers, the recurrence) for
+  // most of each phase.
+  struct DmaBase {
+    uint64_t bw, bk, bu;
+    uint32_t wl, kl, ul;
   };
-  // an out wave's operands for chunk c: Q[t0 + i0 + r][32 g .. + 32], M[i0 + r][16 jb + 4 g .. + 4] (jb ≤ ow), and
-  // γ of the tokens its output lanes hold
+  auto dma_base = [&](uint32_t c, int bf) {
+    const float* in = slot(c);
+    DmaBase d;
+    d.bw = sgpr_ptr(in + kOffW);
+    d.bk = sgpr_ptr(in + kOffKt);
+    d.bu = sgpr_ptr(in + kOffU);
+    d.wl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Wb[bf]);
+    d.kl = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Kb[bf]);
+    d.ul = sgpr_u32((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)Ub[bf]);
+    return d;
+  };
+  const int qw = wave & 3, n0 = 8 * qw;  // a recurrence wave's quarter of the DMA'd tiles
+  // W: LDS chunk 64 n + lane = row 2 n + lane / 32, slot lane % 32
+  auto dma_w = [&](int n) {
+    const int row = 2 * n + (lane >> 5), c4 = (lane & 31) ^ (row & 15);
+    return (uint32_t)((row * DK + 4 * c4) * 4);
+  };
+  // K̃ᵀ: row 4 n + lane / 16, slot lane % 16
+  auto dma_k = [&](int n) {
+    const int row = 4 * n + (lane >> 4), c4 = (lane & 15) ^ (row & 15);
+    return (uint32_t)((row * C + 4 * c4) * 4);
+  };
+  // U rows, columns dv0 .. + 16: row 16 qw + lane / 4, chunk lane % 4
+  const uint32_t u_off = (uint32_t)(((16 * qw + (lane >> 2)) * DK + dv0 + 4 * (lane & 3)) * 4);
+  // The 8 workgroups of a head read the same tiles at about the same time; each starts its 8 contiguous 1 KB
+  // pieces at a different one (rotation by its value-row slice), so that they do not all queue on the same lines.
+  const int rot = (int)blockIdx.y & 7;
+  auto dma_wu = [&](const DmaBase& d) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int p = n0 + ((n + rot) & 7);
+      if (n == 0)
+        dma16_lds<true>(d.wl + p * 1024, dma_w(p), d.bw);
+      else
+        dma16_lds(d.wl + p * 1024, dma_w(p), d.bw);
+    }
+    dma16_lds(d.ul + qw * 1024, u_off, d.bu);
+  };
+  auto dma_kt = [&](const DmaBase& d) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int p = n0 + ((n + rot) & 7);
+      if (n == 0)
+        dma16_lds<true>(d.kl + p * 1024, dma_k(p), d.bk);
+      else
+        dma16_lds(d.kl + p * 1024, dma_k(p), d.bk);
+    }
+  };
+  // an out wave's operands for chunk c: Q[t0 + i0 + r][16 n + 4 g .. + 4] (n < 8: each load instruction reads
+  // 64 contiguous bytes per row, four lanes to a row, where a 32-float run per lane made every lane's 16 bytes a
+  // cache line of its own), M[i0 + r][16 jb + 4 g .. + 4] (jb ≤ ow), and γ of the tokens its output lanes hold
   const int ow = wave - 4, i0 = 16 * ow;
   f4 qa[8], ma[4], gi;  // this chunk's
   f4 qn[8], mn[4], gn;  // the next chunk's, loaded during this one
-  auto load_ops = [&](uint32_t c) {
+  auto load_q = [&](uint32_t c, int n) {
     const uint32_t t = c * C + i0 + r;
-    const float* qr = q + ((size_t)min(t, T - 1) * NK + hk) * DK + 32 * g;  // rows past T: any finite row
-#pragma unroll
-    for (int n = 0; n < 8; ++n) qn[n] = *(const f4*)(qr + 4 * n);
+    const float* qr = q + ((size_t)min(t, T - 1) * NK + hk) * DK + 4 * g;  // rows past T: any finite row
+    qn[n] = *(const f4*)(qr + 16 * n);
+  };
+  auto load_mg = [&](uint32_t c) {
     gn = *(const f4*)(slot(c) + kOffGam + i0 + 4 * g);
     const float* mr = slot(c) + kOffM + (i0 + r) * C + 4 * g;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) mn[jb] = jb <= ow ? *(const f4*)(mr + 16 * jb) : f4{0.f, 0.f, 0.f, 0.f};
   };
+  // The copies happen here, not where the compiler would sink them (the loop's latch, behind the output stores,
+  // with a full wait on them): the empty asm makes each copy's result a value defined at this point.
   auto take_ops = [&]() {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) qa[n] = qn[n];
+    for (int n = 0; n < 8; ++n) {
+      qa[n] = qn[n];
+      asm volatile("" : "+v"(qa[n]));
+    }
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) ma[jb] = mn[jb];
+    for (int jb = 0; jb < 4; ++jb) {
+      ma[jb] = mn[jb];
+      asm volatile("" : "+v"(ma[jb]));
+    }
     gi = gn;
+    asm volatile("" : "+v"(gi));
   };
 
   if (wave >= 4) {
-    dma_chunk(0, 0, ow);
-    load_ops(0);
-    const float gc = slot(0)[kOffGam + C - 1];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) load_q(0, n);
+    load_mg(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     take_ops();
-    if (wave == 4 && lane == 0) Gc[0] = gc;
+    if (wave == 7 && lane == 48) Gc[0] = gi[3];  // γ of the chunk's last token
   } else {
+    const DmaBase d = dma_base(0, 0);
+    dma_wu(d);
+    dma_kt(d);
     for (int e = tid; e < kScanRows * DK / 4; e += 256) {
       const int row = e >> 5, d4 = (e & 31) * 4;
       *(f4*)(Ss + row * LDF + d4) = *(const f4*)(state_in + ((size_t)h * DV + dv0 + row) * DK + d4);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // the recurrence's waves issue first when both waves of a SIMD are ready: the out waves fill the gaps
     __builtin_amdgcn_s_setprio(3);
   }
@@ -522,31 +574,30 @@ __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict
 
   for (uint32_t c = 0; c < nch; ++c) {
     const int bf = c & 1;
-    float gc_next = 0.f;
+    const bool more = c + 1 < nch;
     f4 x;
+    DmaBase dn;
     if (wave >= 4) {
-      if (c + 1 < nch) {
-        dma_chunk(c + 1, bf ^ 1, ow);  // buffer bf ^ 1 was last read during chunk c - 1
-        if (wave == 4) gc_next = slot(c + 1)[kOffGam + C - 1];
-        load_ops(c + 1);
-      }
-      // X[i][dv] = Σ_d Q[i][d] S[dv][d] with S the chunk's starting state
+      // X[i][dv] = Σ_d Q[i][d] S[dv][d] with S the chunk's starting state, the next Q rows loaded between
       f4 sb[8];
-      const float* sr = Ss + r * LDF + 32 * g;
+      const float* sr = Ss + r * LDF + 4 * g;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) sb[n] = *(const f4*)(sr + 4 * n);
+      for (int n = 0; n < 8; ++n) sb[n] = *(const f4*)(sr + 16 * n);
       __builtin_amdgcn_sched_barrier(0);
       f4 x2 = f4{0.f, 0.f, 0.f, 0.f};
       x = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int n = 0; n < 8; ++n)
-#pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          x = mfma4(qa[n][e], sb[n][e], x);
-          x2 = mfma4(qa[n][e + 1], sb[n][e + 1], x2);
+      sfor<0, 16>([&](auto ic) {
+        constexpr int it = decltype(ic)::value, n = it / 2, e = 2 * (it % 2);
+        if constexpr (e == 0) {
+          if (more) load_q(c + 1, n);
         }
+        x = mfma4(qa[n][e], sb[n][e], x);
+        x2 = mfma4(qa[n][e + 1], sb[n][e + 1], x2);
+        __builtin_amdgcn_sched_barrier(0);
+      });
       x = (x + x2) * gi;
     } else {  // V'ᵀ[dv][i] = U[i][dv] − Σ_d S[dv][d] W[i][d]
+      if (more) dn = dma_base(c + 1, bf ^ 1);  // buffers bf ^ 1 were last read during chunk c - 1
       const int iw = 16 * wave;
       const f4 acc = nt_tile_swz<DK, 32>(Ss, LDF, Wb[bf], iw, r, g, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
@@ -554,9 +605,12 @@ __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict
         const int dv = 4 * g + e, i = iw + r;
         Vt[dv * LDT + i] = Ub[bf][i * kScanRows + dv] - acc[e];
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of K̃ᵀ for this chunk (a phase ago)
+      if (more) dma_wu(dn);
     }
-    __syncthreads();  // V'ᵀ complete; every read of S for V' and X done
+    __syncthreads();  // V'ᵀ complete; every read of S for V' and X done; K̃ᵀ in place
     if (wave >= 4) {  // O[i][dv] = γ_i X[i][dv] + Σ_{j ≤ i} M[i][j] V'ᵀ[dv][j]
+      if (more) load_mg(c + 1);
       f4 vb[4];
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) vb[jb] = *(const f4*)(Vt + r * LDT + 16 * jb + 4 * g);
@@ -568,14 +622,15 @@ __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict
           for (int s4 = 0; s4 < 4; ++s4) x = mfma4(ma[jb][s4], vb[jb][s4], x);
         }
       }
-      // the next chunk's tiles and operands have landed (issued a phase ago); the stores below stay in flight
+      // the next chunk's rows have landed; they move into place before the stores go out, so that no wait the
+      // compiler places for those registers (a full one, with stores in flight) falls behind the stores
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      take_ops();
+      if (wave == 7 && lane == 48 && more) Gc[bf ^ 1] = gi[3];  // γ of the next chunk's last token
       const uint32_t tb = c * C + i0 + 4 * g;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (tb + e < T) o[((size_t)(tb + e) * NV + h) * DV + dv0 + r] = x[e];
-      take_ops();
-      if (wave == 4 && lane == 0 && c + 1 < nch) Gc[bf ^ 1] = gc_next;
     } else {  // S[dv][d] ← γ_C S[dv][d] + Σ_j V'ᵀ[dv][j] K̃ᵀ[d][j]; each wave reads and writes only its own columns
       const float gC = Gc[bf];
       const int d0 = 32 * wave;
@@ -590,6 +645,10 @@ __global__ __launch_bounds__(512) void delta_chunk_scan_kernel(float* __restrict
       for (int e = 0; e < 4; ++e) {
         Ss[(4 * g + e) * LDF + d0 + r] = acc0[e];
         Ss[(4 * g + e) * LDF + d0 + 16 + r] = acc1[e];
+      }
+      if (more) {
+        dma_kt(dn);
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wave's W and U for the next chunk; K̃ᵀ in flight
       }
     }
     __syncthreads();  // S and the next chunk's tiles are in place
