@@ -73,8 +73,15 @@ __device__ __forceinline__ void static_for(Fn&& fn) {
 __device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // SwiGLU value silu(g) · u in fp32 (one helper for every epilogue, so all
-// kernels and tilings evaluate it with the same instructions).
-__device__ __forceinline__ float swiglu_f(float g, float u) { return silu_f(g) * u; }
+// kernels and tilings evaluate it with the same instructions). The product
+// is materialised in fp32 (decide rounds it to fp32, then to half): left
+// alone, the compiler may fuse the multiply with the fp16 conversion that
+// follows into one v_fma_mix, which rounds once and so stores other bits.
+__device__ __forceinline__ float swiglu_f(float g, float u) {
+  float v = silu_f(g) * u;
+  asm("" : "+v"(v));
+  return v;
+}
 
 // Keeps an accumulator fragment in AGPRs up to this point of the epilogue, so
 // that the fragments move to VGPRs one at a time as they are stored; left to
