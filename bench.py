@@ -125,6 +125,59 @@ def cpu_baseline(seconds: float):
     }
 
 
+GEMM_WEIGHTS = ("w_in", "w_out", "w_gu", "w_down")
+
+
+def forward_weights(model, layers: int):
+    """The GPU model's embedding, final norm and first `layers` layers on the host, in decide-weights-v1 shapes
+    (GEMM weights widened to fp32 once, exactly: a CPU forward keeps its weights in the type it computes in)."""
+    rows_of = {"embed": 2560, "w_in": 2560, "w_gu": 2560, "w_down": 9216, "conv_w": 4}
+    W = {}
+    for name in model.tensor_names():
+        if name.startswith("L") and int(name[1:name.index(".")]) >= layers:
+            continue
+        a, key = model.download(name), name.split(".")[-1]
+        if key == "w_out":
+            a = a.reshape(2560, -1)
+        elif key in rows_of:
+            a = a.reshape(-1, rows_of[key])
+        W[name] = a.astype(np.float32) if key in GEMM_WEIGHTS else a
+    return W
+
+
+def cpu_forward_sample(W: dict, layers: int, t: int, seconds_cap: float = 120.0):
+    """Config 5 on the host's cores, a reported baseline beside the GPU forward: the oracle's forward
+    (tests/oracle_forward.py: decide's layer order and fp16 rounding points, forward.rs:1118-1310) with every
+    projection on the blocked fp32 GEMM (orc_gemm_f32_fast, OpenMP), over the model's first `layers` layers
+    (3 Gated-DeltaNet + 1 gated attention: the model's 3:1 mix) at t tokens, unpruned; scaled to 36 layers."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_forward
+    import oracle_lib as orc
+    from decide_amd import synth
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    ids = synth.uniform_ids(synth.seed_for(502), t, 151936).astype(np.uint32)
+    ans = np.array([t - 3, t - 2, t - 1], np.uint32)
+    cand = synth.uniform_ids(synth.seed_for(503), 3 * 8, 151936).astype(np.uint32).reshape(3, 8)
+    ncand = np.full(3, 8, np.uint32)
+
+    def gemm(x, w):
+        return orc.gemm_f32_fast(np.asarray(x, np.float32), w, threads)
+
+    t0 = time.perf_counter()
+    lg = oracle_forward.forward(W, layers, ids, ans, cand, ncand, 8, prune=False, gemm=gemm)
+    s = time.perf_counter() - t0
+    assert np.isfinite(lg).all() and s < seconds_cap
+    return {
+        "value": round(s * 1e3 * 36 / layers, 1),
+        "unit": "ms per forward (36 layers, estimated from the sample)",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{layers} of the 36 layers (3 Gated-DeltaNet + 1 gated attention) at {t} tokens, unpruned, "
+                  f"oracle forward with the blocked fp32 GEMM on {threads} threads: {s:.1f} s, scaled by 36/{layers}",
+    }
+
+
 def forward_timing(k, runs: int, with_graph: bool = True):
     """the 4B-shaped hybrid forward (36 layers, 27 Gated-DeltaNet + 9 gated attention,
     d 2560, d_ff 9216, vocab 151,936), random-init fp16 GEMM weights / bf16 embedding / fp32 small
@@ -314,10 +367,14 @@ def main():
         },
         "wall_ms_timed_region": round(wall_ms, 2),
     }
+    cpu_w = forward_weights(fwd_model, 4) if fwd_model is not None and not args.no_cpu_baseline else None
     if fwd_model is not None:
         fwd_model.close()
     if fwd is not None:
         out["forward"] = fwd
+        if cpu_w is not None:
+            fwd["cpu_baseline"] = cpu_forward_sample(cpu_w, 4, 2307)
+            del cpu_w
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:

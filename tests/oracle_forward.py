@@ -35,18 +35,20 @@ def _rope_heads(p: np.ndarray, col: int, heads: int, w: np.ndarray, pos: np.ndar
     return _f16(out)
 
 
-def _mlp(W, pre, x):
+def _mlp(W, pre, x, gemm):
     h = _norm16(x, W[pre + "post_norm"])
-    mlp = _f16(orc.swiglu_interleaved(orc.gemm_nt_f16(h, W[pre + "w_gu"])))
-    return x + orc.gemm_nt_f16(mlp, W[pre + "w_down"])
+    mlp = _f16(orc.swiglu_interleaved(gemm(h, W[pre + "w_gu"])))
+    return x + gemm(mlp, W[pre + "w_down"])
 
 
 def forward(W: dict, layers: int, ids: np.ndarray, ans_rows: np.ndarray, cand: np.ndarray, ncand: np.ndarray,
-            max_cand: int, prune: bool = True) -> np.ndarray:
+            max_cand: int, prune: bool = True, gemm=None) -> np.ndarray:
     """Candidate logits [n_ans, max_cand] (NaN where not written) for a full-route forward from position 0.
 
     W maps decide-weights-v1 names to arrays: fp16 GEMM weights [N, K], fp32 small parameters, and the
-    embedding as raw bf16 bits [vocab, 2560]."""
+    embedding as raw bf16 bits [vocab, 2560]. ``gemm(x, w)`` computes every projection: by default
+    cpu_ref::gemm_nt on the fp16 operands (f64 sums); another correct implementation may be passed."""
+    gemm = gemm or orc.gemm_nt_f16
     t = len(ids)
     pos = np.arange(t, dtype=np.uint32)
     x = orc.embed_bf16(ids, W["embed"])
@@ -56,32 +58,32 @@ def forward(W: dict, layers: int, ids: np.ndarray, ans_rows: np.ndarray, cand: n
         attn = (l + 1) % 4 == 0
         h = _norm16(x, W[pre + "in_norm"])
         if not attn:
-            p = orc.gemm_nt_f16(h, W[pre + "w_in"])
+            p = gemm(h, W[pre + "w_in"])
             q, k, v = orc.conv_silu_l2(p, t, np.zeros((3, orc.CONV_DIM), np.float32), W[pre + "conv_w"])
             o, _ = orc.gated_delta(q, k, v, p[:, LIN_A:LIN_A + NV], p[:, LIN_B:LIN_B + NV], W[pre + "a_log"],
                                    W[pre + "dt_bias"], np.zeros((NV, DV, DK), np.float32), t)
             g = _f16(orc.gated_rmsnorm_silu(o, p[:, LIN_Z:LIN_Z + Q_DIM], W[pre + "gnorm"], t))
         elif prune and l == layers - 1:
             w_in = W[pre + "w_in"]
-            pkv = orc.gemm_nt_f16(h, w_in[ATT_K:])
+            pkv = gemm(h, w_in[ATT_K:])
             kc = _rope_heads(pkv, 0, 4, W[pre + "k_norm"], pos)
             vc = _f16(pkv[:, KV_DIM:].reshape(t, 4, 256))
-            ps = orc.gemm_nt_f16(h[ans_rows], w_in[:ATT_K])
+            ps = gemm(h[ans_rows], w_in[:ATT_K])
             qo = _rope_heads(ps, 0, 16, W[pre + "q_norm"], ans_rows)
             g = _f16(orc.attention(qo.astype(np.float32), ans_rows, kc.astype(np.float32), vc.astype(np.float32),
                                    ps[:, Q_DIM:]))
-            xs = x[ans_rows] + orc.gemm_nt_f16(g, W[pre + "w_out"])
-            xs = _mlp(W, pre, xs)
+            xs = x[ans_rows] + gemm(g, W[pre + "w_out"])
+            xs = _mlp(W, pre, xs, gemm)
             break
         else:
-            p = orc.gemm_nt_f16(h, W[pre + "w_in"])
+            p = gemm(h, W[pre + "w_in"])
             qo = _rope_heads(p, 0, 16, W[pre + "q_norm"], pos)
             kc = _rope_heads(p, ATT_K, 4, W[pre + "k_norm"], pos)
             vc = _f16(p[:, ATT_V:ATT_V + KV_DIM].reshape(t, 4, 256))
             g = _f16(orc.attention(qo.astype(np.float32), pos, kc.astype(np.float32), vc.astype(np.float32),
                                    p[:, Q_DIM:]))
-        x = x + orc.gemm_nt_f16(g, W[pre + "w_out"])
-        x = _mlp(W, pre, x)
+        x = x + gemm(g, W[pre + "w_out"])
+        x = _mlp(W, pre, x, gemm)
     if xs is None:
         xs = x[ans_rows]
     return orc.final_head(xs, W["final_norm"], W["embed"], cand, ncand, max_cand)
