@@ -110,6 +110,34 @@ int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, co
                     "gated_delta (chunked)");
 }
 
+int dh_conv_gated_delta_chunked(dh_ctx* ctx, void* stream, const float* p, const float* prev, const float* w, float* q,
+                                const float* a, const float* b, const float* a_log, const float* dt_bias,
+                                const float* state_in, float* state_out, float* o, uint32_t t, uint32_t ldp,
+                                uint32_t ldab, uint32_t write_state) {
+  if (t < 1) return fail(DH_EINVAL, "conv_delta: T must be at least 1");
+  if (ldp < kConvDim || ldp % 2 != 0)
+    return fail(DH_EINVAL, "conv_delta: ldp = %u must be even and cover the %u qkv columns", ldp, kConvDim);
+  if (ldab < kNV) return fail(DH_EINVAL, "conv_delta: ldab = %u must cover the %u value heads", ldab, kNV);
+  const void* ptrs[] = {p, prev, w, q, a, b, a_log, dt_bias, state_in, state_out, o};
+  const char* names[] = {"p", "prev", "w", "q", "a", "b", "a_log", "dt_bias", "state_in", "state_out", "o"};
+  for (int i = 0; i < 11; ++i) {
+    if (misaligned(ptrs[i], 4)) return fail(DH_EINVAL, "conv_delta: %s address must be a multiple of 4", names[i]);
+    if (!ptrs[i] && !(i == 9 && !write_state)) return fail(DH_EINVAL, "conv_delta: %s is null", names[i]);
+  }
+  if (misaligned(p, 8) || misaligned(prev, 8) || misaligned(w, 16) || misaligned(q, 16) || misaligned(state_in, 16) ||
+      misaligned(state_out, 16))
+    return fail(DH_EINVAL, "conv_delta: p and prev must be 8-byte, w, q and the states 16-byte aligned");
+  if (!ctx) return fail(DH_EINVAL, "conv_delta: null context");
+  // allocates only when T exceeds what dh_warm_up sized the workspace for
+  const int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(t) * sizeof(float));
+  if (rc != DH_OK) return rc;
+  mark(ctx, kKidConvDelta);
+  return hip_status(dh::launch_conv_gated_delta_chunked(p, prev, w, ldp, q, a, b, ldab, a_log, dt_bias, state_in,
+                                                        state_out, o, ctx->aux, t, write_state != 0,
+                                                        (hipStream_t)stream),
+                    "conv + gated_delta (chunked)");
+}
+
 int dh_gated_rmsnorm_silu(dh_ctx* ctx, void* stream, const float* o, const float* z, const float* w, uint16_t* y,
                           uint32_t t, uint32_t ldz) {
   if (ldz < kValueDim || ldz % 2 != 0)

@@ -28,6 +28,7 @@
 // group g holds the contiguous k range [g·K/4, (g + 1)·K/4), so each lane
 // reads its operands with ds_read_b128, all before the MFMAs. Row strides of
 // 4 (mod 64) floats make those reads conflict-free.
+#include "conv_common.h"
 #include "dh_kernels.h"
 
 namespace dh {
@@ -47,6 +48,7 @@ constexpr int kOffGam = kOffKt + DK * C;  // γ [64]
 constexpr int kWsStride = kOffGam + C;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
@@ -112,13 +114,37 @@ __device__ __forceinline__ void lower_block(int p, int& i, int& j) {
 
 }  // namespace
 
+// What prep reads: the conv step's outputs q, k, v, or (fused) the raw
+// in-projection p (row stride ldp, the qkv columns first), the conv state
+// `prev` [3][CONV_DIM] of the rows before the first and the conv weights, from
+// which it forms its own q, k and v (conv_common.h, the stand-alone conv
+// kernel's arithmetic) and writes q for the scan to qout.
+struct PrepSrc {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* p;
+  const float* prev;
+  const float* convw;
+  float* qout;
+  uint32_t ldp;
+};
+
+// Raw conv input row s of channel c (s < 0: the conv state; s ≥ T: zero).
+__device__ __forceinline__ float raw_at(const PrepSrc& in, int s, uint32_t T, uint32_t c) {
+  if (s < 0) return in.prev[(size_t)(3 + s) * convk::CONV_DIM + c];
+  return (uint32_t)s < T ? in.p[(size_t)s * in.ldp + c] : 0.f;
+}
+
 // ---------------------------------------------------------------------------
 // prep: one workgroup per (chunk, key head). The Gram tiles Q Kᵀ and K Kᵀ are
 // the key head's, shared by its two value heads 2 hk and 2 hk + 1 (which
 // differ only in their gates), so they are computed once and scaled for each;
 // then waves 4 hh .. 4 hh + 3 do value head 2 hk + hh's inversion, W and U.
-__global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                               const float* __restrict__ v, const float* __restrict__ a,
+// FUSED: the conv step happens here (see PrepSrc), so k and v never go through
+// memory and the stand-alone conv kernel does not run.
+template <bool FUSED>
+__global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
                                                                const float* __restrict__ b, uint32_t ldab,
                                                                const float* __restrict__ a_log,
                                                                const float* __restrict__ dt_bias, float* __restrict__ ws,
@@ -142,9 +168,38 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const float* __re
   float* const out0 = ws + ((size_t)c * NV + 2 * hk) * kWsStride;
   float* const out = out0 + hh * kWsStride;
 
-  {  // threads 0-255 stage K, 256-511 Q; all loads in flight before the first LDS store
+  if constexpr (FUSED) {
+    // wave w: k (w < 4) or q (w ≥ 4) of key head hk over the chunk's rows 16 (w & 3) .. + 16, lane l owning
+    // channels 2l, 2l + 1: the stand-alone conv kernel's (slot, run) unit, evaluated the same way
+    const int run = wave & 3;
+    const bool isq = wave >= 4;
+    const uint32_t c = (uint32_t)(isq ? hk : NK + hk) * DK + 2 * lane;
+    const f4 w0 = *(const f4*)(src.convw + (size_t)c * 4), w1 = *(const f4*)(src.convw + (size_t)(c + 1) * 4);
+    const int tr0 = (int)t0 + 16 * run;
+    f2 x[19];  // raw rows tr0 - 3 .. tr0 + 15, all loads in flight together
+#pragma unroll
+    for (int j = 0; j < 19; ++j) {
+      const int s = tr0 - 3 + j;
+      if (s < 0)
+        x[j] = *(const f2*)(src.prev + (size_t)(3 + s) * convk::CONV_DIM + c);
+      else
+        x[j] = (uint32_t)s < T ? *(const f2*)(src.p + (size_t)s * src.ldp + c) : f2{0.f, 0.f};
+    }
+    float* dst = isq ? R2 : Ks;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const uint32_t t = (uint32_t)(tr0 + u);
+      const float y0 = convk::conv_silu(w0, x[u][0], x[u + 1][0], x[u + 2][0], x[u + 3][0]);
+      const float y1 = convk::conv_silu(w1, x[u][1], x[u + 1][1], x[u + 2][1], x[u + 3][1]);
+      const float inv = convk::l2_inv(y0, y1);
+      const float sc = isq ? convk::q_scale(inv) : inv;
+      const f2 o = t < T ? f2{y0 * sc, y1 * sc} : f2{0.f, 0.f};
+      *(f2*)(dst + (16 * run + u) * LDF + 2 * lane) = o;
+      if (isq && t < T) *(f2*)(src.qout + ((size_t)t * NK + hk) * DK + 2 * lane) = o;
+    }
+  } else {  // threads 0-255 stage K, 256-511 Q; all loads in flight before the first LDS store
     f4 x[8];
-    fetch_rows(x, tid < 256 ? k : q, t0, T, NK, hk, tid & 255);
+    fetch_rows(x, tid < 256 ? src.k : src.q, t0, T, NK, hk, tid & 255);
     stage_rows(tid < 256 ? Ks : R2, x, tid & 255);
   }
   if (lw == 0) {  // waves 0 and 4: value head h's gates
@@ -223,17 +278,29 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const float* __re
   if (tid < 2 * C) out0[(tid >> 6) * kWsStride + kOffGam + (tid & 63)] = Gm[tid >> 6][tid & 63];
 
   // This wave's U operand, V[t0 + 16 jb + 4 g + s][16 (2 lw + q2) + r], straight into registers; the loads
-  // run during the inversion below.
+  // run during the inversion below (fused: its 4 tokens' 7 raw rows per block, conv + SiLU in registers).
   f4 vr[2][4];
+  f4 vw[2];          // fused: the conv weights of this wave's two value channels
+  float vx[2][4][7];  // fused: raw rows 16 jb + 4 g - 3 .. + 3 of them, combined after the inversion
 #pragma unroll
-  for (int q2 = 0; q2 < 2; ++q2)
+  for (int q2 = 0; q2 < 2; ++q2) {
+    if constexpr (FUSED) {
+      const uint32_t c = 2 * convk::KEY_DIM + h * DV + 16 * (2 * lw + q2) + r;
+      vw[q2] = *(const f4*)(src.convw + (size_t)c * 4);
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
+      for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const uint32_t t = t0 + 16 * jb + 4 * g + s4;
-        vr[q2][jb][s4] = t < T ? v[((size_t)t * NV + h) * DV + 16 * (2 * lw + q2) + r] : 0.f;
-      }
+        for (int j = 0; j < 7; ++j) vx[q2][jb][j] = raw_at(src, (int)t0 + 16 * jb + 4 * g - 3 + j, T, c);
+    } else {
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const uint32_t t = t0 + 16 * jb + 4 * g + s4;
+          vr[q2][jb][s4] = t < T ? src.v[((size_t)t * NV + h) * DV + 16 * (2 * lw + q2) + r] : 0.f;
+        }
+    }
+  }
 
   // T = (I + A)⁻¹ per value head, blocked 4 × 4 over 16 × 16 blocks. Diagonal blocks by forward
   // substitution (wave lw of the head's half, lane j < 16 owns column j of block lw); then the blocks below
@@ -282,6 +349,19 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const float* __re
       for (int e = 0; e < 4; ++e) Ts[(16 * i + 4 * g + e) * LDT + 16 * j + r] = -z[e];
     }
     __syncthreads();
+  }
+
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const float* x = vx[q2][jb];
+          vr[q2][jb][s4] = t0 + 16 * jb + 4 * g + s4 < T ? convk::conv_silu(vw[q2], x[s4], x[s4 + 1], x[s4 + 2], x[s4 + 3])
+                                                         : 0.f;
+        }
   }
 
   // W = T diag(βγ) K and U = T diag(β) V. Wave lw of the head's half: key/value columns 16 td for td = 2 lw,
@@ -668,8 +748,23 @@ hipError_t launch_gated_delta_chunked(const float* q, const float* k, const floa
                                       float* state_out, float* o, float* ws, uint32_t t, uint32_t ldab,
                                       bool write_state, hipStream_t s) {
   const uint32_t nch = (t + C - 1) / C;
-  hipLaunchKernelGGL(delta_chunk_prep_kernel, dim3(nch, NK), dim3(512), 0, s, q, k, v, a, b, ldab, a_log, dt_bias, ws,
-                     t);
+  const PrepSrc src{q, k, v, nullptr, nullptr, nullptr, nullptr, 0};
+  hipLaunchKernelGGL(delta_chunk_prep_kernel<false>, dim3(nch, NK), dim3(512), 0, s, src, a, b, ldab, a_log, dt_bias,
+                     ws, t);
+  hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(512), 0, s, ws, q, state_in, state_out, o,
+                     t, write_state ? 1u : 0u);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv_gated_delta_chunked(const float* p, const float* prev, const float* conv_w, uint32_t ldp,
+                                           float* q, const float* a, const float* b, uint32_t ldab,
+                                           const float* a_log, const float* dt_bias, const float* state_in,
+                                           float* state_out, float* o, float* ws, uint32_t t, bool write_state,
+                                           hipStream_t s) {
+  const uint32_t nch = (t + C - 1) / C;
+  const PrepSrc src{nullptr, nullptr, nullptr, p, prev, conv_w, q, ldp};
+  hipLaunchKernelGGL(delta_chunk_prep_kernel<true>, dim3(nch, NK), dim3(512), 0, s, src, a, b, ldab, a_log, dt_bias,
+                     ws, t);
   hipLaunchKernelGGL(delta_chunk_scan_kernel, dim3(NV, DV / kScanRows), dim3(512), 0, s, ws, q, state_in, state_out, o,
                      t, write_state ? 1u : 0u);
   return hipGetLastError();

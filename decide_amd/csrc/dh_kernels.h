@@ -94,6 +94,14 @@ hipError_t launch_gated_delta_chunked(const float* q, const float* k, const floa
                                       const float* a_log, const float* dt_bias, const float* state_in,
                                       float* state_out, float* o, float* ws, uint32_t t, uint32_t ldab,
                                       bool write_state, hipStream_t s);
+// The conv step fused into the chunked recurrence: from the raw in-projection
+// p (row stride ldp), the conv state `prev` [3][8192] and the conv weights;
+// q (the conv step's q output) is written for the scan, k and v are not.
+hipError_t launch_conv_gated_delta_chunked(const float* p, const float* prev, const float* conv_w, uint32_t ldp,
+                                           float* q, const float* a, const float* b, uint32_t ldab,
+                                           const float* a_log, const float* dt_bias, const float* state_in,
+                                           float* state_out, float* o, float* ws, uint32_t t, bool write_state,
+                                           hipStream_t s);
 hipError_t launch_gated_rmsnorm_silu(const float* o, const float* z, const float* w, _Float16* y, uint32_t t,
                                      uint32_t ldz, hipStream_t s);
 hipError_t launch_q_norm_rope(const float* pq, const float* qw, const float* inv_freq, const uint32_t* qpos,

@@ -112,6 +112,11 @@ void source_of(dh_model* m, Source src, uint32_t i, const float** conv, const fl
   }
 }
 
+// Whether dh_gated_delta runs the chunked recurrence for t rows on this context (its own rule).
+bool delta_chunked(const dh_ctx* ctx, uint32_t t) {
+  return (ctx->flags & DH_DELTA_CHUNKED) || (!(ctx->flags & DH_DELTA_SEQUENTIAL) && t >= DH_DELTA_CHUNK_MIN_T);
+}
+
 // The recurrence over chunk rows from..to, from state_in to state_out (forward.rs:1208-1216).
 int delta(dh_model* m, void* s, const Layer& L, uint32_t from, uint32_t to, const float* state_in, float* state_out,
           bool write) {
@@ -132,23 +137,33 @@ int layer_full(dh_model* m, void* s, const Layer& L, const Chunk& ch, Source src
     const float* conv_in = m->conv[i];
     const float* state_in = m->state[i];
     if (ch.first) source_of(m, src, i, &conv_in, &state_in);
-    TRY(dh_conv_silu_l2(m->ctx, s, m->p, conv_in, as<float>(L.conv_w->ptr), m->q, m->k, m->v, rows, LIN_IN_N));
     const bool capture = entry && ch.capture;
-    // the capture's update reads conv_in before the in-place update below may overwrite it
-    if (capture) TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, entry->conv[i].as<float>(), ch.capture, LIN_IN_N));
-    if (ch.keep_state) TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, m->conv[i], rows, LIN_IN_N));
-    if (capture) {
-      // split at the end of the state: the state there goes to the entry, and the
-      // rest of the chunk continues from it (fp32 through memory, so exactly)
-      float* at = entry->state[i].as<float>();
-      TRY(delta(m, s, L, 0, ch.capture, state_in, at, true));
-      if (ch.capture < rows)
-        TRY(delta(m, s, L, ch.capture, rows, at, m->state[i], ch.keep_state));
-      else if (ch.keep_state)
-        TRY(hip_status(hipMemcpyAsync(m->state[i], at, kStateBytes, hipMemcpyDeviceToDevice, (hipStream_t)s),
-                       "state copy"));
+    if (!capture && delta_chunked(m->ctx, rows)) {
+      // conv and the chunked recurrence in one call (the prep kernel forms q, k, v itself); then the conv state,
+      // whose in-place update must follow every read of conv_in
+      TRY(dh_conv_gated_delta_chunked(m->ctx, s, m->p, conv_in, as<float>(L.conv_w->ptr), m->q, m->p + LIN_A,
+                                      m->p + LIN_B, as<float>(L.a_log->ptr), as<float>(L.dt_bias->ptr), state_in,
+                                      m->state[i], m->o, rows, LIN_IN_N, LIN_IN_N, ch.keep_state ? 1u : 0u));
+      if (ch.keep_state) TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, m->conv[i], rows, LIN_IN_N));
     } else {
-      TRY(delta(m, s, L, 0, rows, state_in, m->state[i], ch.keep_state));
+      TRY(dh_conv_silu_l2(m->ctx, s, m->p, conv_in, as<float>(L.conv_w->ptr), m->q, m->k, m->v, rows, LIN_IN_N));
+      // the capture's update reads conv_in before the in-place update below may overwrite it
+      if (capture)
+        TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, entry->conv[i].as<float>(), ch.capture, LIN_IN_N));
+      if (ch.keep_state) TRY(dh_conv_state_update(m->ctx, s, m->p, conv_in, m->conv[i], rows, LIN_IN_N));
+      if (capture) {
+        // split at the end of the state: the state there goes to the entry, and the
+        // rest of the chunk continues from it (fp32 through memory, so exactly)
+        float* at = entry->state[i].as<float>();
+        TRY(delta(m, s, L, 0, ch.capture, state_in, at, true));
+        if (ch.capture < rows)
+          TRY(delta(m, s, L, ch.capture, rows, at, m->state[i], ch.keep_state));
+        else if (ch.keep_state)
+          TRY(hip_status(hipMemcpyAsync(m->state[i], at, kStateBytes, hipMemcpyDeviceToDevice, (hipStream_t)s),
+                         "state copy"));
+      } else {
+        TRY(delta(m, s, L, 0, rows, state_in, m->state[i], ch.keep_state));
+      }
     }
     TRY(dh_gated_rmsnorm_silu(m->ctx, s, m->o, m->p + LIN_Z, as<float>(L.gnorm->ptr), (uint16_t*)m->g, rows,
                               LIN_IN_N));

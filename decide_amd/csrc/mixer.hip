@@ -10,6 +10,7 @@
 // tokens and bound by its per-token dependency chain.
 #include <type_traits>
 
+#include "conv_common.h"
 #include "dh_kernels.h"
 
 namespace dh {
@@ -50,7 +51,8 @@ __device__ __forceinline__ float row16_sum(float v) {
 // ---------------------------------------------------------------------------
 // conv + SiLU + L2. One wave per (slot, run of 16 rows): slots 0-15 are q
 // heads, 16-31 k heads, 32-63 v heads (128 channels each); lane l owns
-// channels 2l, 2l + 1 of the slot. The wave loads the run's 16 rows and the 3
+// channels 2l, 2l + 1 of the slot. The arithmetic is conv_common.h's, which
+// the chunked recurrence's prep kernel evaluates too when it fuses this step. The wave loads the run's 16 rows and the 3
 // before it once (raw rows before the chunk come from `prev` [3][CONV_DIM]),
 // all loads in flight together, and slides the 4-tap window over them; each
 // output is the same fma chain as a single-row evaluation. Grid: (64 slots,
@@ -79,20 +81,15 @@ __global__ __launch_bounds__(256) void conv_silu_l2_kernel(const float* __restri
   for (int u = 0; u < kConvRun; ++u) {
     const uint32_t t = t0 + u;
     if (t >= T) break;
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a0 = fmaf(w0[j], x[u + j][0], a0);
-      a1 = fmaf(w1[j], x[u + j][1], a1);
-    }
-    const float y0 = silu_fast(a0), y1 = silu_fast(a1);
+    const float y0 = convk::conv_silu(w0, x[u][0], x[u + 1][0], x[u + 2][0], x[u + 3][0]);
+    const float y1 = convk::conv_silu(w1, x[u][1], x[u + 1][1], x[u + 2][1], x[u + 3][1]);
     if (slot >= 32) {
       *(f2*)(v + ((size_t)t * NV + (slot - 32)) * DV + 2 * lane) = f2{y0, y1};
       continue;
     }
-    const float inv = rsqrtf(wave_sum(y0 * y0 + y1 * y1) + 1e-6f);
+    const float inv = convk::l2_inv(y0, y1);
     if (slot < 16) {
-      const float sc = inv * 0.08838834764831845f;  // DK^-1/2
+      const float sc = convk::q_scale(inv);
       *(f2*)(q + ((size_t)t * NK + slot) * DK + 2 * lane) = f2{y0 * sc, y1 * sc};
     } else {
       *(f2*)(k + ((size_t)t * NK + (slot - 16)) * DK + 2 * lane) = f2{y0 * inv, y1 * inv};

@@ -236,6 +236,16 @@ class Delta:
                                       addr(b), addr(a_log), addr(dt_bias), addr(state_in), addr(state_out), addr(o),
                                       t, ldab, 1 if write_state else 0))
 
+    def conv_gated_delta_chunked(self, stream: int, p: Arg, prev: Arg, w: Arg, q: Arg, a: Arg, b: Arg, a_log: Arg,
+                                 dt_bias: Arg, state_in: Arg, state_out: Arg, o: Arg, t: int, ldp: int, ldab: int,
+                                 write_state: bool) -> None:
+        """``Conv::conv_silu_l2`` then ``gated_delta`` in one call on the chunked recurrence (only q is written
+        of the conv outputs)."""
+        _call(self.lib.dh_conv_gated_delta_chunked(self.ctx.handle, ctypes.c_void_p(stream), addr(p), addr(prev),
+                                                   addr(w), addr(q), addr(a), addr(b), addr(a_log), addr(dt_bias),
+                                                   addr(state_in), addr(state_out), addr(o), t, ldp, ldab,
+                                                   1 if write_state else 0))
+
 
 class GNorm:
     """decide's ``GNorm`` (kernels/gnorm.rs:10-31)."""

@@ -248,6 +248,22 @@ int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, co
                    const float* b, const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
                    float* o, uint32_t t, uint32_t ldab, uint32_t write_state);
 
+/* decide: Conv::conv_silu_l2 then Delta::gated_delta on its outputs
+ * (kernels/conv.rs:20-35, kernels/delta.rs:53-80; forward.rs:1203-1216), in one
+ * call on the chunked recurrence: its prep kernel forms q, k and v from p, prev
+ * and w itself, with dh_conv_silu_l2's arithmetic, so k and v never go through
+ * memory. Results are bitwise those of dh_conv_silu_l2 followed by
+ * dh_gated_delta on the chunked path, and q (the only conv output the rest of
+ * the recurrence reads) is written as dh_conv_silu_l2 writes it. Arguments as
+ * there: p's qkv columns 0..8192 of t rows (row stride ldp, even, >= 8192),
+ * prev [3, 8192], w [8192, 4]; a, b rows of stride ldab; q [t, 16, 128] out.
+ * Always the chunked path, whatever the context's DH_DELTA_* flags; p and prev
+ * 8-byte, w, q and the states 16-byte aligned. */
+int dh_conv_gated_delta_chunked(dh_ctx* ctx, void* stream, const float* p, const float* prev, const float* w, float* q,
+                                const float* a, const float* b, const float* a_log, const float* dt_bias,
+                                const float* state_in, float* state_out, float* o, uint32_t t, uint32_t ldp,
+                                uint32_t ldab, uint32_t write_state);
+
 /* decide: GNorm::gated_rmsnorm_silu (kernels/gnorm.rs:19-31; cpu_ref.rs:132-145).
  * y fp16 [t, 4096] = per (row, value head) RMSNorm of o over 128 dims with
  * weight w (fp32 [128], no +1), times silu(z); z rows of stride ldz. */

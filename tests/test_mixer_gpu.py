@@ -155,6 +155,34 @@ def test_gated_delta_in_place_chunks_and_no_write(gpu, kernels_delta_sequential,
     assert np.isnan(untouched).all(), "write_state = 0 must leave state_out untouched"
 
 
+@pytest.mark.parametrize("t", [1, 70, 2307])
+def test_conv_gated_delta_chunked_equals_the_two_steps(gpu, kernels_delta_chunked, stream, t):
+    """dh_conv_gated_delta_chunked, whose prep kernel forms q, k and v from p itself, against dh_conv_silu_l2 then
+    dh_gated_delta on the chunked path: q, o and the final state bit for bit, from a nonzero conv state (raw rows
+    before the first) and a nonzero state; t = 70 and 2,307 end inside a chunk."""
+    ks = kernels_delta_chunked
+    p = synth.normal_f32(synth.seed_for(190), (t, LIN_IN_N), 1.0)
+    prev = synth.normal_f32(synth.seed_for(191), (3, CONV_DIM), 1.0)
+    w = synth.normal_f32(synth.seed_for(192), (CONV_DIM, 4), 0.5)
+    a_log = synth.normal_f32(synth.seed_for(193), (NV,), 0.5)
+    dt_bias = synth.normal_f32(synth.seed_for(194), (NV,), 0.5)
+    s0 = synth.normal_f32(synth.seed_for(195), (NV, DV, DK), 0.05)
+    pd, prevd, wd, ad, dd, sd = (to_dev(x) for x in (p, prev, w, a_log, dt_bias, s0))
+    q1, k1, v1 = (empty(s, np.float32) for s in ((t, NK, DK), (t, NK, DK), (t, NV, DV)))
+    o1, o2 = empty((t, NV, DV), np.float32), empty((t, NV, DV), np.float32)
+    s1, s2 = full(s0.shape, np.float32, np.nan), full(s0.shape, np.float32, np.nan)
+    q2 = full((t, NK, DK), np.float32, np.nan)
+    ks.conv.conv_silu_l2(stream, (pd, 0), (prevd, 0), (wd, 0), (q1, 0), (k1, 0), (v1, 0), t, LIN_IN_N)
+    ks.delta.gated_delta(stream, (q1, 0), (k1, 0), (v1, 0), (pd, LIN_A * 4), (pd, LIN_B * 4), (ad, 0), (dd, 0),
+                         (sd, 0), (s1, 0), (o1, 0), t, LIN_IN_N, True)
+    ks.delta.conv_gated_delta_chunked(stream, (pd, 0), (prevd, 0), (wd, 0), (q2, 0), (pd, LIN_A * 4),
+                                      (pd, LIN_B * 4), (ad, 0), (dd, 0), (sd, 0), (s2, 0), (o2, 0), t, LIN_IN_N,
+                                      LIN_IN_N, True)
+    sync()
+    for name, a, b in (("q", q1, q2), ("o", o1, o2), ("state", s1, s2)):
+        np.testing.assert_array_equal(to_host(b).view(np.uint32), to_host(a).view(np.uint32), err_msg=name)
+
+
 @pytest.mark.parametrize("t", [1, 33])
 def test_gated_rmsnorm_silu_matches_oracle(gpu, kernels, stream, t):
     o = synth.normal_f32(synth.seed_for(160), (t, NV, DV), 1.0)

@@ -99,6 +99,25 @@ def test_chunked_full_route_matches_oracle(gpu, model, weights):
         _close(got, one, ROUTE_TOL)
 
 
+def test_chunks_carry_the_conv_state_into_the_fused_recurrence(gpu, kernels_delta_chunked, weights):
+    """On a context that always runs the chunked recurrence, every chunk of a Gated-DeltaNet layer takes the fused
+    conv + recurrence call, which reads the carried conv state and only then lets the next chunk's state replace it:
+    chunked requests still match the oracle's whole-sequence forward."""
+    m = Model(kernels_delta_chunked.ctx, CFG)
+    kernels_delta_chunked.gemm.warm_up(0, max_m=CFG.max_tokens)
+    m.init_random(0, seed=2024)  # the module model's weights, so `weights` is its oracle copy
+    sync()
+    try:
+        ids = _ids(90, 1)
+        answers = _answers([89, 40, 61], 10)
+        want = _oracle(weights, ids, answers)
+        for chunk in (90, 17, 40):
+            m.set_chunk(chunk)
+            _close(m.logits_full(0, ids, answers), want, ORACLE_TOL)
+    finally:
+        m.close()
+
+
 def test_unpruned_chunked_matches_pruned(gpu, model):
     ids = _ids(70, 2)
     answers = _answers([30, 69], 20)
