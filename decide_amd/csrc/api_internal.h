@@ -35,7 +35,7 @@ namespace dh_api {
 
 // Kernel ids for dh_variants_loaded beyond the tile menu (ids < kMaxTileVariants);
 // every id is below 64, one bit of dh_ctx::used each.
-constexpr int kMaxTileVariants = 16;
+constexpr int kMaxTileVariants = 24;
 enum : int {
   kKidReduce = kMaxTileVariants, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
   kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny,

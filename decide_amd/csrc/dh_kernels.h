@@ -46,9 +46,10 @@ struct VariantInfo {
   int fn;  // 16-column fragments per wave
   int wn;  // waves along N
   int wm;  // waves along M
+  int spw = 1;  // waves per wave position (2: each position's block split between two waves of one SIMD)
   int bm() const { return 16 * fm * wm; }
   int bn() const { return 16 * fn * wn; }
-  int waves() const { return wm * wn; }
+  int waves() const { return wm * wn * spw; }
 };
 
 // The small-M weight-streaming kernel (gemm_stream.hip) over the members of

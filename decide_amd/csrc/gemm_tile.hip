@@ -770,6 +770,380 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 void gemm_tile22_kernel(const TileArgs p) {
   tile_body<FM, FN, 2, NBX, NBW>(p);
 }
+// ---------------------------------------------------------------------------
+// 8-wave BM x BN tiles, two waves per SIMD (BM = 32·FM, BN = 32·(FNA + FNB)). A wave
+// reads LDS at about 32 bytes per clock however many reads it keeps in
+// flight, so four waves draw at most ~128 B/clk from a CU's LDS, which serves
+// about twice that to eight; and eight waves store an epilogue with twice the
+// threads. The 2 x 2 tile's quadrants (BM/2 x BN/2) are each split between the
+// two waves of one SIMD: BM/2 x 16·FNA ("wide", waves 0-3) and BM/2 x 16·FNB
+// ("narrow", waves 4-7); wave w runs on SIMD w % 4 and takes quadrant
+// (w % 4 / 2, w % 2). Every output still gets its MFMAs in the same K order
+// as in Pipe, so these tiles store the same bits as the other variants.
+// A stage's DMAs (BM/8 X row groups of 8 rows, then BN/8 W groups) go to the
+// waves round-robin: DMA D belongs to wave D % 8. With 256 x 256 the two rings
+// (X 2 deep, W 3 deep) fill the whole 160 KB of LDS.
+// DMAs of each kind that wave w (of 8) issues per stage, for NG groups starting at group B
+constexpr int t8_count(int w, int B, int NG) {
+  int c = 0;
+  for (int D = w; D < B + NG; D += 8) c += D >= B;
+  return c;
+}
+
+template <int FM_, int FN, int XPW, int WPW, int BN>
+struct Pipe8 {
+  static constexpr int FM = FM_, NBX = 2, NBW = 3, LAX = 1, LAW = 2, U = 6;
+  static constexpr int XBYTES = 32 * FM * 128, WBYTES = BN * 128, WRING = NBX * XBYTES;
+  static constexpr int LDS_BYTES = NBX * XBYTES + NBW * WBYTES;
+  static constexpr int DPW = XPW + WPW;
+  static constexpr int KEEP = WPW;  // at a stage's end: stage kt + 2's W DMAs stay in flight
+  static_assert(XPW >= 1 && WPW >= 1 && KEEP + DPW <= 63, "DMAs per wave");
+
+  f4 acc[FM][FN];
+  uint32_t doff[DPW];  // per-lane source byte offsets (X row groups, then W row groups)
+  uint32_t dlds[DPW];  // LDS byte offset of each group inside its ring slot (wave-uniform)
+  uint32_t a0, a1, xrow, wrow, lds_addr;
+  const char* wbase;
+  const char* xbase;
+
+  template <int D, int NX, int NW>
+  __device__ __forceinline__ void dma_one(int kx, int kw) {
+    if constexpr (D < XPW)
+      dma16(lds_addr + NX * XBYTES + dlds[D], doff[D], xbase + (size_t)kx * (kBK * 2));
+    else
+      dma16(lds_addr + WRING + NW * WBYTES + dlds[D], doff[D], wbase + (size_t)kw * (kBK * 2));
+  }
+  template <int B>
+  __device__ __forceinline__ void dma_x(int kt) {
+    static_for<0, XPW>([&](auto dc) { dma_one<decltype(dc)::value, B, 0>(kt, 0); });
+  }
+  template <int B>
+  __device__ __forceinline__ void dma_w(int kt) {
+    static_for<XPW, DPW>([&](auto dc) { dma_one<decltype(dc)::value, 0, B>(0, kt); });
+  }
+  template <int BX, int BW>
+  __device__ __forceinline__ void issue(int kt, int nst) {
+    if (kt + LAX < nst) dma_x<(BX + LAX) % NBX>(kt + LAX);
+    if (kt + LAW < nst) dma_w<(BW + LAW) % NBW>(kt + LAW);
+  }
+  __device__ __forceinline__ void wait_next(int kt, int nst, bool steady) {
+    if (steady || kt + LAW < nst)
+      wait_vm<KEEP>();
+    else
+      wait_vm<0>();
+  }
+
+  // The streamed schedule of Pipe::stage_s, for this wave's FM x FN block.
+  static constexpr bool RA = FM <= FN;
+  static constexpr int NR = RA ? FM : FN, NS = RA ? FN : FM;
+  static constexpr int NG = 2 * NS, NL = 2 * (NR + NS);
+  static constexpr int LAG = 3, NB = 3, GB = NG - NB;
+  static constexpr int need(int g) { return (g / NS) * (NR + NS) + NR + g % NS; }
+  static constexpr int issued(int g) {
+    const int la = g < NS ? LAG : LAG + 1;
+    return need(g + la < NG - 1 ? g + la : NG - 1) + 1;
+  }
+  static constexpr int ENTRY = need(LAG - 1) + 1;
+  static_assert(NS > LAG + 1 && GB >= 2 && issued(GB - 1) == NL, "streamed schedule");
+
+  h8 rf[2][NR], sf[2][NS];
+
+  template <int I, int BX, int BW>
+  __device__ __forceinline__ void read_one() {
+    constexpr int h = I / (NR + NS), q = I % (NR + NS);
+    constexpr bool isr = q < NR;
+    constexpr int f = isr ? q : q - NR;
+    constexpr bool isx = isr == RA;
+    const uint32_t kh = h ? a1 : a0;
+    const uint32_t base = isx ? lds_addr + BX * XBYTES + xrow + kh : lds_addr + WRING + BW * WBYTES + wrow + kh;
+    if constexpr (isr)
+      ds_read16<f * 16 * 128>(rf[h][f], base);
+    else
+      ds_read16<f * 16 * 128>(sf[h][f], base);
+  }
+  template <int B, int E, int BX, int BW>
+  __device__ __forceinline__ void read_range() {
+    static_for<B, E>([&](auto ic) { read_one<decltype(ic)::value, BX, BW>(); });
+  }
+  template <int BX, int BW>
+  __device__ __forceinline__ void entry_reads() {
+    read_range<0, ENTRY, BX, BW>();
+  }
+  template <int Q>
+  __device__ __forceinline__ void stage_s(int kt, int nst, bool steady) {
+    constexpr int BX = Q % NBX, BW = Q % NBW;
+    constexpr int NX = (Q + 1) % NBX, NW = (Q + 1) % NBW;
+    constexpr int NXS = (BX + LAX) % NBX, NWS = (BW + LAW) % NBW;
+    constexpr int NEED = XPW;  // X (lookahead 1) is needed by stage kt + 1: issued at group 0
+    constexpr int REST = DPW - NEED;
+    if (!steady) issue<BX, BW>(kt, nst);
+    static_for<0, NG>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      constexpr int h = g / NS, s = g % NS;
+      if constexpr (g == GB) {
+        wait_lgkm<0>();
+        if (kt + 1 < nst) wait_next(kt, nst, steady);
+        __syncthreads();
+        if (kt + 1 < nst) entry_reads<NX, NW>();
+      }
+      if constexpr (g < GB) {
+        static_for<0, DPW>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          constexpr int at = d < NEED ? 0 : 1 + (d - NEED) * (GB - 1) / REST;
+          if constexpr (at == g) {
+            if (steady) dma_one<d, NXS, NWS>(kt + LAX, kt + LAW);
+          }
+        });
+        read_range<g == 0 ? ENTRY : issued(g - 1), issued(g), BX, BW>();
+        constexpr int pending = issued(g) - need(g) - 1;
+        wait_lgkm<(pending < 15 ? pending : 15)>();
+        tie(sf[h][s]);
+        if constexpr (s == 0) {
+#pragma unroll
+          for (int r = 0; r < NR; ++r) tie(rf[h][r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if constexpr (RA)
+          mfma_acc_v(acc[r][s], rf[h][r], sf[h][s]);
+        else
+          mfma_acc_v(acc[s][r], sf[h][s], rf[h][r]);
+      }
+    });
+  }
+};
+
+// Epilogue of the 8-wave tile, through LDS in fp32 (row stride 292 floats):
+// 64 rows at a time, each wave writes its fragments of those rows, then all
+// 512 threads store whole rows with 16-byte stores (SwiGLU reads each
+// 8-column output chunk's gate and up halves back from the staged rows).
+template <int FM, int FN, int BN>
+__device__ __forceinline__ void store_tile8(f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split, uint32_t m0,
+                                            uint32_t n0, int rbase, int cbase, int r, int g, float* stage) {
+  constexpr int LDR = BN + 4, CR = 64, NT = 512, BM = 32 * FM;
+  const uint32_t M = p.m, N = p.mem[mi].n;
+  const int tid = threadIdx.x;
+  const uint32_t epi = p.mem[mi].epi, ldy = p.mem[mi].ldy;
+  char* Y = (char*)p.mem[mi].y;
+  const bool partial = p.splits > 1;
+  const uint32_t esz = (partial || epi == 0u || epi == 2u) ? 4u : 2u;
+  const bool vec16 = partial || ((((uintptr_t)Y) % 16) == 0 && ((size_t)ldy * esz) % 16 == 0);
+  static_for<0, (BM + CR - 1) / CR>([&](auto cc) {
+    constexpr int c0 = decltype(cc)::value * CR;
+    constexpr int rows = (BM - c0) < CR ? (BM - c0) : CR;
+    if (m0 + c0 >= M) return;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int tr = rbase + 16 * i;  // fragments never straddle a CR boundary
+      if (tr < c0 || tr >= c0 + CR) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        pin_acc(acc[i][j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stage[(tr - c0 + 4 * g + e) * LDR + cbase + j * 16 + r] = acc[i][j][e];
+      }
+    }
+    __syncthreads();
+    if (epi == 3u && !partial) {
+      // output chunk q of a row: columns 8q .. 8q + 7 of the fp16 [.., N/2] output
+      constexpr int OQ = BN / 16;
+#pragma unroll
+      for (int it = 0; it < (rows * OQ + NT - 1) / NT; ++it) {
+        const int item = it * NT + tid;
+        if (item >= rows * OQ) break;
+        const int row = item / OQ, q = item % OQ;
+        const uint32_t grow = m0 + c0 + row;
+        const int gc = 32 * (q / 2) + 8 * (q % 2);
+        if (grow >= M || n0 + 32 * (q / 2) >= N) continue;
+        const float* sr = stage + row * LDR + gc;
+        const f4 g0 = *(const f4*)sr, g1 = *(const f4*)(sr + 4);
+        const f4 u0 = *(const f4*)(sr + 16), u1 = *(const f4*)(sr + 20);
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = (_Float16)swiglu_f(g0[e], u0[e]);
+          o[4 + e] = (_Float16)swiglu_f(g1[e], u1[e]);
+        }
+        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + 8 * q;
+        if (vec16) {
+          __builtin_nontemporal_store(o, (h8*)dst);
+        } else {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) *(h2*)(dst + e) = h2{o[e], o[e + 1]};
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int it = 0; it < (rows * (BN / 4) + NT - 1) / NT; ++it) {
+      const int item = it * NT + tid;
+      if (item >= rows * (BN / 4)) break;
+      const int row = item / (BN / 4), cq = item % (BN / 4);
+      const uint32_t grow = m0 + c0 + row, gcol = n0 + 4 * cq;
+      if (grow >= M || gcol >= N) continue;
+      const f4 v = *(const f4*)(stage + row * LDR + 4 * cq);
+      if (partial) {
+        __builtin_nontemporal_store(v, (f4*)(p.ws + ((size_t)split * M + grow) * N + gcol));
+      } else if (epi == 1u) {
+        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + gcol;
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        *(h2*)dst = h2{(_Float16)v[0], (_Float16)v[1]};
+        *(h2*)(dst + 2) = h2{(_Float16)v[2], (_Float16)v[3]};
+      } else {
+        float* dst = (float*)Y + (size_t)grow * ldy + gcol;
+        typedef float fl2 __attribute__((ext_vector_type(2)));
+        if (vec16) {
+          f4 o = v;
+          if (epi == 2u) o += *(const f4*)dst;
+          *(f4*)dst = o;
+        } else {
+          fl2 lo = fl2{v[0], v[1]}, hi = fl2{v[2], v[3]};
+          if (epi == 2u) {
+            lo += *(const fl2*)dst;
+            hi += *(const fl2*)(dst + 2);
+          }
+          *(fl2*)dst = lo;
+          *(fl2*)(dst + 2) = hi;
+        }
+      }
+    }
+  });
+}
+
+// One wave's share of the 8-wave tile: FN fragments per wave (FNA or FNB), its DMAs per stage.
+template <int FM, int FN, int FNA, int FNB, int W0>
+__device__ __forceinline__ void tile8_wave(const TileArgs& p, char* lds, int wave, int mi, uint32_t m0, uint32_t n0,
+                                           uint32_t split, int nst, bool half_tail, uint32_t ldw, uint32_t N,
+                                           uint32_t kb) {
+  constexpr int BN = 32 * (FNA + FNB), XG = 4 * FM;  // X row groups of 8 rows
+  constexpr int XPW = t8_count(W0, 0, XG), WPW = t8_count(W0, XG, BN / 8);
+  static_assert(t8_count(W0, 0, XG) == t8_count(W0 + 3, 0, XG) && t8_count(W0, XG, BN / 8) == t8_count(W0 + 3, XG, BN / 8),
+                "the four waves of one path issue the same DMA counts");
+  using P = Pipe8<FM, FN, XPW, WPW, BN>;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t M = p.m;
+  const int simd = wave & 3, mh = simd >> 1, nq = 2 * (simd & 1) + (wave >> 2);
+  const int rbase = 16 * FM * mh, cbase = 16 * (FNA + FNB) * (nq >> 1) + 16 * FNA * (nq & 1);
+  P pp;
+  pp.lds_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  pp.wbase = (const char*)(p.mem[mi].w + kb);
+  pp.xbase = (const char*)(p.x + kb);
+  const uint32_t sw = (uint32_t)((r >> 1) & 7);
+  pp.a0 = r * 128 + ((g ^ sw) * 16);
+  pp.a1 = r * 128 + (((4 + g) ^ sw) * 16);
+  pp.xrow = (uint32_t)rbase * 128;
+  pp.wrow = (uint32_t)cbase * 128;
+#pragma unroll
+  for (int d = 0; d < P::DPW; ++d) {
+    const int D = wave + 8 * d;                // global DMA index: X groups, then W groups
+    const int G = d < XPW ? D : D - XG;        // row group inside its operand
+    const uint32_t row = 8 * G + (lane >> 3);  // tile-local row
+    const uint32_t chunk = (uint32_t)((lane & 7) ^ ((row >> 1) & 7));
+    if (d < XPW)
+      pp.doff[d] = (min(m0 + row, M - 1) * p.ldx + chunk * 8) * 2;
+    else
+      pp.doff[d] = (min(n0 + row, N - 1) * ldw + chunk * 8) * 2;
+    pp.dlds[d] = (uint32_t)G * 1024;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) pp.acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  if (nst > 0) {
+    pp.template dma_x<0>(0);
+    pp.template dma_w<0>(0);
+    if (nst > 1) {
+      pp.template dma_w<1>(1);
+      wait_vm<WPW>();
+    } else {
+      wait_vm<0>();
+    }
+    __syncthreads();
+    pp.template entry_reads<0, 0>();
+    int kt = 0;
+    for (; kt + P::U - 1 + P::LAW < nst; kt += P::U) {
+      static_for<0, P::U>([&](auto qc) { pp.template stage_s<decltype(qc)::value>(kt + decltype(qc)::value, nst, true); });
+    }
+    static_for<0, P::U + P::LAW>([&](auto qc) {
+      constexpr int qq = decltype(qc)::value;
+      if (kt + qq < nst) pp.template stage_s<qq % P::U>(kt + qq, nst, false);
+    });
+  }
+  if (half_tail) {  // K % 64 == 32: one 32-wide sub-stage into slot 0, unpipelined
+    const char* xb = pp.xbase + (size_t)nst * (kBK * 2);
+    const char* wb = pp.wbase + (size_t)nst * (kBK * 2);
+#pragma unroll
+    for (int d = 0; d < P::DPW; ++d) {
+      const int D = wave + 8 * d, G = d < XPW ? D : D - XG;
+      const uint32_t chunk = (uint32_t)((lane & 7) ^ (((8 * G + (lane >> 3)) >> 1) & 7));
+      if (chunk < 4) {
+        if (d < XPW)
+          dma16(pp.lds_addr + pp.dlds[d], pp.doff[d], xb);
+        else
+          dma16(pp.lds_addr + P::WRING + pp.dlds[d], pp.doff[d], wb);
+      }
+    }
+    wait_vm<0>();
+    __syncthreads();
+    const uint32_t b0 = pp.lds_addr + pp.xrow + pp.a0;
+    const uint32_t w0 = pp.lds_addr + P::WRING + pp.wrow + pp.a0;
+    h8 wf[FN];
+    static_for<0, FN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      ds_read16<j * 16 * 128>(wf[j], w0);
+    });
+    static_for<0, FM>([&](auto fc) {
+      constexpr int i = decltype(fc)::value;
+      h8 a;
+      ds_read16<i * 16 * 128>(a, b0);
+      wait_lgkm<0>();
+      tie(a);
+      if constexpr (i == 0) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) tie(wf[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) mfma_acc_v(pp.acc[i][j], a, wf[j]);
+    });
+  }
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  store_tile8<FM, FN, BN>(pp.acc, p, mi, split, m0, n0, rbase, cbase, r, g, (float*)lds);
+}
+
+template <int FM, int FNA, int FNB>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+void gemm_tile8_kernel(const TileArgs p) {
+  constexpr int BN = 32 * (FNA + FNB), BM = 32 * FM;
+  constexpr int LDSB = 2 * BM * 128 + 3 * BN * 128;
+  static_assert(LDSB <= 160 * 1024, "the rings fit the LDS");
+  static_assert(LDSB >= 64 * (BN + 4) * 4, "the epilogue's staging fits the rings");
+  __shared__ __attribute__((aligned(1024))) char lds[LDSB];
+  const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t mt = wid % p.mtiles;
+  const uint32_t q = wid / p.mtiles;
+  const uint32_t gs = q % p.nstripes;
+  const uint32_t split = q / p.nstripes;
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxMembers; ++i)
+    if (i < (int)p.count && gs >= p.mem[i].stripe_begin) mi = i;
+  const uint32_t ldw = p.mem[mi].ldw, N = p.mem[mi].n;
+  const uint32_t m0 = mt * BM, n0 = (gs - p.mem[mi].stripe_begin) * BN;
+  const uint32_t kb = split * p.kps;
+  const uint32_t ke = min(p.k, kb + p.kps);
+  const int nst = (int)((ke - kb) / kBK);
+  const bool half_tail = ((ke - kb) % kBK) != 0;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (wave < 4)
+    tile8_wave<FM, FNA, FNA, FNB, 0>(p, lds, wave, mi, m0, n0, split, nst, half_tail, ldw, N, kb);
+  else
+    tile8_wave<FM, FNB, FNA, FNB, 4>(p, lds, wave, mi, m0, n0, split, nst, half_tail, ldw, N, kb);
+}
 
 // ---- the compiled menu: (FM, NBX, NBW). BM = 16·FM rows, BN = 256.
 #define DH_TILE_MENU(X) \
@@ -803,16 +1177,19 @@ static const VariantEntry kVariants[] = {
     {{5, 5, 2, 2}, gemm_tile22_kernel<5, 5, 3, 3>},
     // 128 x 96 with a 5-deep ring: medium M (96-490 rows) over narrow N
     {{4, 3, 2, 2}, gemm_tile22_kernel<4, 3, 5, 5>},
+    // 8 waves, two per SIMD: 256 x 256 and 256 x 224, the wide M = 2307 projections in under three rounds
+    {{8, 8, 2, 2, 2}, gemm_tile8_kernel<8, 4, 4>},
+    {{8, 7, 2, 2, 2}, gemm_tile8_kernel<8, 4, 3>},
 };
 #undef DH_TILE_ENTRY
 
-static_assert(sizeof(kVariants) / sizeof(kVariants[0]) <= 16, "the C ABI numbers other kernels from 16 on");
+static_assert(sizeof(kVariants) / sizeof(kVariants[0]) <= 24, "kernel ids from 24 on name the other kernels");
 int variant_count() { return (int)(sizeof(kVariants) / sizeof(kVariants[0])); }
 VariantInfo variant_info(int v) { return kVariants[v].info; }
 
 hipError_t launch_tile(int v, const TileArgs& a, uint32_t grid, hipStream_t s) {
   const VariantEntry& e = kVariants[v];
-  hipLaunchKernelGGL(e.fn, dim3(grid), dim3(64 * e.info.wn * e.info.wm), 0, s, a);
+  hipLaunchKernelGGL(e.fn, dim3(grid), dim3(64 * e.info.waves()), 0, s, a);
   return hipGetLastError();
 }
 

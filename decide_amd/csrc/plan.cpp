@@ -61,8 +61,8 @@ const Measured kMeasured[] = {
     {2560, 12352, 276, 10, 1},  // 35.54 us
     {2560, 12352, 490, 8, 1},  // 44.43 us
     {2560, 12352, 603, 4, 1},  // 48.46 us
-    {2560, 12352, 1024, 6, 1},  // 67.87 us
-    {2560, 12352, 2307, 5, 1},  // 153.76 us
+    {2560, 12352, 1024, 17, 1},  // 67.2 us (8-wave 256 x 224; 72.1 for 208 x 256 beside it)
+    {2560, 12352, 2307, 16, 1},  // 146.9 us (8-wave 256 x 256; 159.6 for the 160 x 256 tile beside it)
     {2560, 10240, 1, 0, 4},  // 15.56 us
     {2560, 10240, 3, 0, 4},  // 15.69 us
     {2560, 10240, 8, 0, 4},  // 16.18 us
@@ -75,7 +75,7 @@ const Measured kMeasured[] = {
     {2560, 10240, 490, 14, 1},  // 37.89 us
     {2560, 10240, 603, 14, 1},  // 41.27 us
     {2560, 10240, 1024, 9, 1},  // 58.28 us
-    {2560, 10240, 2307, 6, 1},  // 132.6 us; set from the 36-layer forward (see the header)
+    {2560, 10240, 2307, 17, 1},  // 126.0 us (8-wave 256 x 224; 134.5 for 208 x 256 beside it)
     {2560, 18432, 1, 0, 3},  // 22.01 us
     {2560, 18432, 3, 0, 3},  // 22.27 us
     {2560, 18432, 8, 0, 3},  // 22.66 us
@@ -88,7 +88,7 @@ const Measured kMeasured[] = {
     {2560, 18432, 490, 9, 1},  // 50.79 us
     {2560, 18432, 603, 11, 1},  // 56.4 us
     {2560, 18432, 1024, 5, 1},  // 90.81 us
-    {2560, 18432, 2307, 9, 1},  // 206.3 us; with the next row, set from the 36-layer forward (see the header)
+    {2560, 18432, 2307, 16, 1},  // 194.2 us (8-wave 256 x 256; 209.6 for 176 x 256 beside it)
     {4096, 2560, 1, 0, 8},  // 12.91 us
     {4096, 2560, 3, 0, 8},  // 13.32 us
     {4096, 2560, 8, 0, 8},  // 13.54 us

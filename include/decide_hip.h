@@ -149,7 +149,9 @@ int dh_gemm_ws_need(const dh_ctx* ctx, uint32_t max_m, uint32_t n, uint32_t k, u
 /* Forces the next GEMMs on this context to use `variant` and `splits`
  * (variant = UINT32_MAX restores the planner). For tuning sweeps only. */
 int dh_gemm_force(dh_ctx* ctx, uint32_t variant, uint32_t splits);
-/* Number of compiled tile variants and the geometry of one of them. */
+/* Number of compiled tile variants and the geometry of one of them: the tile's
+ * rows and columns, its wavefronts (4, or 8 with two per SIMD) and the columns
+ * of one wave position (with 8 waves, the two waves of a SIMD split it). */
 uint32_t dh_gemm_variant_count(void);
 int dh_gemm_variant_info(uint32_t variant, uint32_t* bm, uint32_t* bn, uint32_t* waves, uint32_t* wave_cols);
 
