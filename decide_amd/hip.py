@@ -10,7 +10,7 @@ allocation and timing event in a single HIP instance.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_size_t, c_uint, c_void_p
+from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_size_t, c_uint, c_uint32, c_void_p
 
 import numpy as np
 
@@ -41,6 +41,7 @@ def rt() -> ctypes.CDLL:
         "hipStreamDestroy": (c_int, [c_void_p]),
         "hipStreamSynchronize": (c_int, [c_void_p]),
         "hipEventCreate": (c_int, [POINTER(c_void_p)]),
+        "hipEventCreateWithFlags": (c_int, [POINTER(c_void_p), c_uint32]),
         "hipEventDestroy": (c_int, [c_void_p]),
         "hipEventRecord": (c_int, [c_void_p, c_void_p]),
         "hipEventSynchronize": (c_int, [c_void_p]),
@@ -152,10 +153,21 @@ class Stream:
             self.handle = None
 
 
+# hipEventDisableSystemFence: the event's record skips the system-scope fence (an L2 write-back and
+# invalidate) that a default event performs, which would stall the stream and leave the next kernel a cold L2.
+EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+
+
 class Event:
-    def __init__(self):
+    """A HIP event. ``timing=True`` makes a timing-only event (no system-scope fence on record): for
+    timestamps between kernels of one stream, read after a default event later on that stream completes."""
+
+    def __init__(self, timing: bool = False):
         h = c_void_p()
-        check(rt().hipEventCreate(byref(h)), "hipEventCreate")
+        if timing:
+            check(rt().hipEventCreateWithFlags(byref(h), EVENT_DISABLE_SYSTEM_FENCE), "hipEventCreateWithFlags")
+        else:
+            check(rt().hipEventCreate(byref(h)), "hipEventCreate")
         self.handle = h.value
 
     def record(self, stream: int = 0) -> None:
