@@ -144,18 +144,22 @@ __device__ __forceinline__ float raw_at(const PrepSrc& in, int s, uint32_t T, ui
 // FUSED: the conv step happens here (see PrepSrc), so k and v never go through
 // memory and the stand-alone conv kernel does not run.
 template <bool FUSED>
-__global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(4, 4))) void
+delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
                                                                const float* __restrict__ b, uint32_t ldab,
                                                                const float* __restrict__ a_log,
                                                                const float* __restrict__ dt_bias, float* __restrict__ ws,
                                                                uint32_t T) {
-  // 112 KB of LDS, one workgroup of 8 waves per CU: Q is staged only for the Gram tiles, whose results wait in
-  // registers until every wave is past them; then each value head's A and T take Q's place. V never goes
-  // through LDS (each wave loads its U operand into registers during the inversion).
+  // 78 KB of LDS, so that two workgroups of 8 waves fit a CU: Q is staged only for the Gram tiles, whose results
+  // wait in registers until every wave is past them; then each value head's A and T take Q's place, sharing one
+  // [64][68] tile: A (strictly lower) in the blocks below the diagonal, Tᵀ in the blocks above it, and each
+  // diagonal 16 × 16 block holding A_jj until its forward substitution replaces it with the whole T_jjᵀ (A_jj is
+  // read by nothing else). V never goes through LDS (each wave loads its U operand into registers during the
+  // inversion).
   constexpr int kAT = C * LDT;  // one [64][68] tile
-  constexpr int kR2 = C * LDF > 4 * kAT ? C * LDF : 4 * kAT;
+  constexpr int kR2 = C * LDF > 2 * kAT ? C * LDF : 2 * kAT;
   __shared__ __attribute__((aligned(16))) float Ks[C * LDF];
-  __shared__ __attribute__((aligned(16))) float R2[kR2];  // Q; then A0 | T0 | A1 | T1
+  __shared__ __attribute__((aligned(16))) float R2[kR2];  // Q; then A0 + T0ᵀ | A1 + T1ᵀ
   __shared__ __attribute__((aligned(16))) float Lg[2][C], Bt[2][C], Gm[2][C], SCw[2][C], Rh[2][C];
   __shared__ float Ysc[8 * 16 * 17];  // per-wave 16 × 16 scratch of the blocked inversion
   const uint32_t c = blockIdx.x, hk = blockIdx.y, t0 = c * C;
@@ -163,8 +167,7 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
   const int r = lane & 15, g = lane >> 4;
   const int hh = wave >> 2, lw = wave & 3;  // this wave's value head (of the key head's two), and its wave in that half
   const uint32_t h = 2 * hk + hh;
-  float* const As = R2 + 2 * hh * kAT;
-  float* const Ts = As + kAT;
+  float* const ATs = R2 + hh * kAT;  // A[i][j] at [i][j], T[i][j] at [j][i] (see above)
   float* const out0 = ws + ((size_t)c * NV + 2 * hk) * kWsStride;
   float* const out = out0 + hh * kWsStride;
 
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
           const int i = 16 * ti + 4 * g + e;
           const float rr = i >= j ? expf(Lg[vh][i] - Lg[vh][j]) : 0.f;
           if (!isq)
-            R2[2 * vh * kAT + i * LDT + j] = i > j ? Bt[vh][i] * rr * gacc[u][e] : 0.f;
+            R2[vh * kAT + i * LDT + j] = i > j ? Bt[vh][i] * rr * gacc[u][e] : 0.f;
           else
             out0[vh * kWsStride + kOffM + i * C + j] = rr * gacc[u][e];
         }
@@ -307,7 +310,6 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
   // the diagonal, one block-diagonal at a time,
   //   T_ij = −T_ii Σ_{k=j}^{i−1} A_ik T_kj,
   // as 16 × 16 MFMA products through a per-wave LDS scratch block.
-  for (int e = tid; e < 2 * kAT; e += 512) R2[(2 * (e / kAT) + 1) * kAT + e % kAT] = 0.f;
   __syncthreads();
   {
     const int jb = lw;
@@ -318,13 +320,13 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
         float sacc = 0.f;
         sfor<0, i>([&](auto mc) {
           constexpr int m = decltype(mc)::value;
-          sacc = fmaf(As[(16 * jb + i) * LDT + 16 * jb + m], x[m], sacc);
+          sacc = fmaf(ATs[(16 * jb + i) * LDT + 16 * jb + m], x[m], sacc);
         });
         x[i] = i == lane ? 1.0f : -sacc;
       });
-      sfor<0, 16>([&](auto ic) {
+      sfor<0, 16>([&](auto ic) {  // column lane of T_jj as row lane of T_jjᵀ, over A_jj (every read of it is done)
         constexpr int i = decltype(ic)::value;
-        Ts[(16 * jb + i) * LDT + 16 * jb + lane] = x[i];
+        ATs[(16 * jb + lane) * LDT + 16 * jb + i] = x[i];
       });
     }
   }
@@ -335,8 +337,8 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
       f4 y = f4{0.f, 0.f, 0.f, 0.f};
       for (int kb = j; kb < i; ++kb) {  // Y = Σ_k A_ik T_kj
 #pragma unroll
-        for (int kk = 0; kk < 16; kk += 4)
-          y = mfma4(As[(16 * i + r) * LDT + 16 * kb + kk + g], Ts[(16 * kb + kk + g) * LDT + 16 * j + r], y);
+        for (int kk = 0; kk < 16; kk += 4)  // A[16 i + r][16 kb + kk + g] T[16 kb + kk + g][16 j + r]
+          y = mfma4(ATs[(16 * i + r) * LDT + 16 * kb + kk + g], ATs[(16 * j + r) * LDT + 16 * kb + kk + g], y);
       }
       float* Yw = Ysc + wave * 16 * 17;
 #pragma unroll
@@ -344,9 +346,10 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
       __builtin_amdgcn_wave_barrier();
       f4 z = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < 16; kk += 4) z = mfma4(Ts[(16 * i + r) * LDT + 16 * i + kk + g], Yw[(kk + g) * 17 + r], z);
+      for (int kk = 0; kk < 16; kk += 4)  // T[16 i + r][16 i + kk + g]
+        z = mfma4(ATs[(16 * i + kk + g) * LDT + 16 * i + r], Yw[(kk + g) * 17 + r], z);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Ts[(16 * i + 4 * g + e) * LDT + 16 * j + r] = -z[e];
+      for (int e = 0; e < 4; ++e) ATs[(16 * j + r) * LDT + 16 * i + 4 * g + e] = -z[e];
     }
     __syncthreads();
   }
@@ -380,7 +383,9 @@ __global__ __launch_bounds__(512) void delta_chunk_prep_kernel(const PrepSrc src
         f4 ta[ti + 1], sv[ti + 1], rb[ti + 1];
 #pragma unroll
         for (int jb = 0; jb <= ti; ++jb) {
-          ta[jb] = *(const f4*)(Ts + (16 * ti + r) * LDT + 16 * jb + 4 * g);
+#pragma unroll
+          for (int s = 0; s < 4; ++s)  // T[16 ti + r][16 jb + 4 g + s]
+            ta[jb][s] = ATs[(16 * jb + 4 * g + s) * LDT + 16 * ti + r];
           sv[jb] = *(const f4*)(sc + 16 * jb + 4 * g);
           if (isu) {
             rb[jb] = vr[q2][jb];
