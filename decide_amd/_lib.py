@@ -112,6 +112,11 @@ PROTOTYPES = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_uint32,
          c_uint32, c_float],
     ),
+    "dh_gemm_add_rmsnorm": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_void_p, c_uint32, c_uint32, c_uint32,
+         c_uint32, c_void_p, c_uint32, c_float, c_void_p, c_uint32],
+    ),
     "dh_fill_normal_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_float]),
     "dh_interleave_gate_up": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),
     "dh_deinterleave_q_gate": (c_int, [c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]),

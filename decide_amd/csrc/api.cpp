@@ -141,9 +141,12 @@ dh::Plan choose_plan(const dh_ctx* c, uint32_t m, uint32_t n, uint32_t k, uint32
 }
 
 // Enqueues plan p. Split-K partials go to `fixed_ws` when given (it must hold
-// p.ws_bytes), else to the context's workspace, grown if needed.
+// p.ws_bytes), else to the context's workspace, grown if needed. With
+// `partials_out`, a split plan stops after the tile kernel and returns where
+// its partials are, for the caller to reduce.
 int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint32_t ldx, uint32_t m, uint32_t k,
-                const dh_gemm_member* mem, uint32_t count, float* fixed_ws = nullptr) {
+                const dh_gemm_member* mem, uint32_t count, float* fixed_ws = nullptr,
+                const float** partials_out = nullptr) {
   dh::TileArgs a{};
   a.x = (const _Float16*)x;
   a.ldx = ldx;
@@ -192,6 +195,10 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
     rc = hip_status(dh::launch_tile(p.variant, a, grid, s), "gemm tile kernel launch");
   }
   if (rc != DH_OK || p.splits == 1) return rc;
+  if (partials_out) {
+    *partials_out = a.ws;
+    return rc;
+  }
   mark(c, kKidReduce);
   return hip_status(dh::launch_splitk_reduce(a.ws, p.splits, m, mem[0].n, mem[0].y, mem[0].ldy, mem[0].epi, s),
                     "split-K reduce launch");
@@ -261,6 +268,36 @@ int dh_gemm_nt(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const voi
   if (p.variant < 0) return fail(DH_EINVAL, "gemm: no plan for M = %u, N = %u, K = %u", m, n, k);
   dh_gemm_member mem{w, y, ldw, ldy, n, epi};
   return launch_plan(ctx, s, p, x, ldx, m, k, &mem, 1);
+}
+
+int dh_gemm_add_rmsnorm(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, float* y,
+                        uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, const float* norm_w, uint32_t add_one,
+                        float eps, uint16_t* h, uint32_t ldh) {
+  int rc = check_gemm(ctx, x, ldx, w, ldw, y, ldy, m, n, k, DH_EPI_ADD_F32);
+  if (rc != DH_OK) return rc;
+  if (!ctx) return fail(DH_EINVAL, "gemm_add_rmsnorm: null context");
+  if (n == 0) return fail(DH_EINVAL, "gemm_add_rmsnorm: N must be at least 32 (a row to normalise)");
+  if (n > ldh) return fail(DH_EINVAL, "gemm_add_rmsnorm: N = %u exceeds ldh = %u", n, ldh);
+  if (m && (!norm_w || !h)) return fail(DH_EINVAL, "gemm_add_rmsnorm: null norm weight or output");
+  hipStream_t s = (hipStream_t)stream;
+  if (!(ctx->flags & DH_GEMM_REFERENCE) && m && k) {
+    const dh::Plan p = choose_plan(ctx, m, n, k, DH_EPI_ADD_F32);
+    if (p.variant >= 0 && p.splits > 1 && dh::splitk_add_rmsnorm_fits(p.splits, n, ldy, ldh, y, norm_w, h)) {
+      dh_gemm_member mem{w, y, ldw, ldy, n, DH_EPI_ADD_F32};
+      const float* partials = nullptr;
+      rc = launch_plan(ctx, s, p, x, ldx, m, k, &mem, 1, nullptr, &partials);
+      if (rc != DH_OK) return rc;
+      mark(ctx, kKidAddNorm);
+      return hip_status(dh::launch_splitk_add_rmsnorm(partials, p.splits, m, n, y, ldy, norm_w, (_Float16*)h, ldh,
+                                                      add_one != 0, eps, s),
+                        "split-K add + rmsnorm launch");
+    }
+  }
+  rc = dh_gemm_nt(ctx, stream, x, ldx, w, ldw, y, ldy, m, n, k, DH_EPI_ADD_F32);
+  if (rc != DH_OK) return rc;
+  mark(ctx, kKidNorm);
+  return hip_status(dh::launch_rmsnorm_rows(y, norm_w, (_Float16*)h, nullptr, m, n, ldy, ldh, add_one != 0, eps, s),
+                    "rmsnorm_rows");
 }
 
 static_assert(dh::kNoAllocScratchBytes == DH_NOALLOC_SCRATCH_BYTES, "the header states the scratch size");

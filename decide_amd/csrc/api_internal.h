@@ -39,7 +39,7 @@ constexpr int kMaxTileVariants = 24;
 enum : int {
   kKidReduce = kMaxTileVariants, kKidReference, kKidGather32, kKidGather16, kKidHead, kKidNorm, kKidFill,
   kKidConv, kKidConvState, kKidDelta, kKidGNorm, kKidQRope, kKidKVRope, kKidAttn, kKidEmbed, kKidFillAny,
-  kKidDeltaChunk, kKidStream, kKidAttnCombine, kKidConvDelta, kKidCount
+  kKidDeltaChunk, kKidStream, kKidAttnCombine, kKidConvDelta, kKidAddNorm, kKidCount
 };
 static_assert(kKidCount <= 64, "kernel ids must fit dh_ctx::used");
 

@@ -77,6 +77,13 @@ hipError_t launch_final_head(const float* x, const float* w, const uint16_t* tab
                              uint32_t max_cand, float eps, hipStream_t s);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, _Float16* y, const uint32_t* rowmap, uint32_t rows,
                                uint32_t h, uint32_t ld_in, uint32_t ld_out, bool add_one, float eps, hipStream_t s);
+// x[r] += Σ_s ws[s][r] (split-K partials [splits][rows][h], split order), then y[r] = rmsnorm(x[r]): bitwise the
+// split-K reduce's AddF32 followed by launch_rmsnorm_rows, for the shapes splitk_add_rmsnorm_fits accepts.
+bool splitk_add_rmsnorm_fits(uint32_t splits, uint32_t h, uint32_t ldx, uint32_t ldy, const void* x, const void* w,
+                             const void* y);
+hipError_t launch_splitk_add_rmsnorm(const float* ws, uint32_t splits, uint32_t rows, uint32_t h, float* x,
+                                     uint32_t ldx, const float* w, _Float16* y, uint32_t ldy, bool add_one, float eps,
+                                     hipStream_t s);
 hipError_t launch_fill_normal_f16(uint16_t* out, uint64_t n, uint64_t seed, float std, hipStream_t s);
 hipError_t launch_fill_normal(void* out, uint64_t n, uint64_t seed, float mean, float sd, uint32_t dtype,
                               hipStream_t s);

@@ -87,11 +87,21 @@ int gemm(dh_model* m, void* s, const void* x, uint32_t ldx, const void* w, uint3
   return dh_gemm_nt(m->ctx, s, x, ldx, w, ldw, y, ldy, rows, n, k, epi);
 }
 
-// x += MLP(norm(x)) over `rows` rows (decide: encode_mlp without the ANE split, forward.rs:1272-1282).
-int mlp(dh_model* m, void* s, const Layer& L, float* x, _Float16* h, uint32_t rows) {
-  TRY(norm(m, s, x, L.post_norm, h, rows));
+// x += a·wᵀ over `rows` rows (a fp16 [rows, k]), then h = rmsnorm(x) with weight nw when one is given: the
+// residual add of a projection and the norm that reads the new x next, as one call (dh_gemm_add_rmsnorm, one
+// kernel for both where the projection splits K).
+int add_norm(dh_model* m, void* s, const void* a, const Tensor* w, float* x, uint32_t rows, uint32_t k,
+             const Tensor* nw, _Float16* h) {
+  if (!nw) return gemm(m, s, a, k, w->ptr, k, x, HIDDEN, rows, HIDDEN, k, DH_EPI_ADD_F32);
+  return dh_gemm_add_rmsnorm(m->ctx, s, a, k, w->ptr, k, x, HIDDEN, rows, HIDDEN, k, as<float>(nw->ptr), 1, EPS,
+                             (uint16_t*)h, HIDDEN);
+}
+
+// x += MLP(h) over `rows` rows, h = norm(x, post_norm) on entry (decide: encode_mlp without the ANE split,
+// forward.rs:1272-1282); then h = norm(x, next) when the next layer's input norm is given.
+int mlp(dh_model* m, void* s, const Layer& L, float* x, _Float16* h, uint32_t rows, const Tensor* next) {
   TRY(gemm(m, s, h, HIDDEN, L.w_gu->ptr, HIDDEN, m->mlp, INTER, rows, MLP_IN_N, HIDDEN, DH_EPI_SWIGLU_F16));
-  return gemm(m, s, m->mlp, INTER, L.w_down->ptr, INTER, x, HIDDEN, rows, HIDDEN, INTER, DH_EPI_ADD_F32);
+  return add_norm(m, s, m->mlp, L.w_down, x, rows, INTER, next, h);
 }
 
 // The (conv, recurrent) state chunk 0 of a run reads for linear layer i (decide: source, forward.rs:1036-1046).
@@ -127,10 +137,11 @@ int delta(dh_model* m, void* s, const Layer& L, uint32_t from, uint32_t to, cons
                         LIN_IN_N, write ? 1u : 0u);
 }
 
-// Layer L over every row of the chunk (decide: encode_layer, forward.rs:1189-1268).
-int layer_full(dh_model* m, void* s, const Layer& L, const Chunk& ch, Source src, const StateEntry* entry) {
+// Layer L over every row of the chunk (decide: encode_layer, forward.rs:1189-1268). On entry h = norm(x, in_norm)
+// (formed by the previous layer's last projection); on exit h = norm(x, next) when `next` is given.
+int layer_full(dh_model* m, void* s, const Layer& L, const Chunk& ch, Source src, const StateEntry* entry,
+               const Tensor* next) {
   const uint32_t rows = ch.rows;
-  TRY(norm(m, s, m->x, L.in_norm, m->h, rows));
   if (!L.attn) {
     const uint32_t i = L.lin_index;
     TRY(gemm(m, s, m->h, HIDDEN, L.w_in->ptr, HIDDEN, m->p, LIN_IN_N, rows, LIN_IN_N, HIDDEN, DH_EPI_STORE_F32));
@@ -178,8 +189,8 @@ int layer_full(dh_model* m, void* s, const Layer& L, const Chunk& ch, Source src
                               (const uint16_t*)m->vc[L.att_index], m->p, qpos, (uint16_t*)m->g, rows, ATT_IN_N,
                               ch.pos0 + rows));
   }
-  TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, m->x, HIDDEN, rows, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
-  return mlp(m, s, L, m->x, m->h, rows);
+  TRY(add_norm(m, s, m->g, L.w_out, m->x, rows, VALUE_DIM, L.post_norm, m->h));
+  return mlp(m, s, L, m->x, m->h, rows, next);
 }
 
 // Final norm + candidate logits of the chunk's answers from xs (decide: encode_final_head, forward.rs:1296-1306).
@@ -191,10 +202,9 @@ int final_head(dh_model* m, void* s, const RunArgs& r, const Chunk& ch) {
 }
 
 // The last layer (full attention) pruned to the chunk's answer rows
-// (decide: encode_last_layer_pruned, forward.rs:1133-1187).
+// (decide: encode_last_layer_pruned, forward.rs:1133-1187). On entry h = norm(x, in_norm) over the chunk's rows.
 int layer_pruned(dh_model* m, void* s, const Layer& L, const RunArgs& r, const Chunk& ch) {
   const _Float16* w_in = as<_Float16>(L.w_in->ptr);
-  TRY(norm(m, s, m->x, L.in_norm, m->h, ch.rows));
   // rows ATT_K.. of w_in are k|v
   TRY(gemm(m, s, m->h, HIDDEN, w_in + (size_t)ATT_K * HIDDEN, HIDDEN, m->p, 2 * KV_DIM, ch.rows, 2 * KV_DIM, HIDDEN,
            DH_EPI_STORE_F32));
@@ -216,8 +226,8 @@ int layer_pruned(dh_model* m, void* s, const Layer& L, const RunArgs& r, const C
                             (const uint16_t*)m->vc[L.att_index], ps, qpos, (uint16_t*)m->g, n, ATT_K,
                             ch.pos0 + ch.rows));
   TRY(dh_gather_rows_f32(m->ctx, s, m->x, rowmap, xs, n, HIDDEN));
-  TRY(gemm(m, s, m->g, VALUE_DIM, L.w_out->ptr, VALUE_DIM, xs, HIDDEN, n, HIDDEN, VALUE_DIM, DH_EPI_ADD_F32));
-  TRY(mlp(m, s, L, xs, hs, n));
+  TRY(add_norm(m, s, m->g, L.w_out, xs, n, VALUE_DIM, L.post_norm, hs));
+  TRY(mlp(m, s, L, xs, hs, n, nullptr));
   return final_head(m, s, r, ch);
 }
 
@@ -228,9 +238,10 @@ int dh_model_impl::encode_chunk(dh_model* m, void* s, const RunArgs& r, const Ch
   TRY(dh_embed_bf16(m->ctx, s, r.ids + ch.stage_row, (const uint16_t*)m->embed->ptr, m->x, ch.rows, HIDDEN));
   const uint32_t last = m->cfg.layers - 1;
   prune = prune && is_full_attention(last);
-  for (uint32_t l = 0; l < last; ++l) TRY(layer_full(m, s, m->layers[l], ch, src, capture));
+  TRY(norm(m, s, m->x, m->layers[0].in_norm, m->h, ch.rows));
+  for (uint32_t l = 0; l < last; ++l) TRY(layer_full(m, s, m->layers[l], ch, src, capture, m->layers[l + 1].in_norm));
   if (prune) return layer_pruned(m, s, m->layers[last], r, ch);
-  TRY(layer_full(m, s, m->layers[last], ch, src, capture));
+  TRY(layer_full(m, s, m->layers[last], ch, src, capture, nullptr));
   if (ch.n == 0) return ok();
   TRY(dh_gather_rows_f32(m->ctx, s, m->x, r.ans_rows + ch.a0, m->xs + (size_t)ch.a0 * HIDDEN, ch.n, HIDDEN));
   return final_head(m, s, r, ch);

@@ -128,14 +128,15 @@ hipError_t launch_final_head(const float* x, const float* w, const uint16_t* tab
 }
 
 // ---------------------------------------------------------------------------
-// y[r] = half(x[rowmap[r]] · rsqrt(mean(x²) + eps) · w'), w' = 1 + w or w.
+// y[r] = half(x[rowmap[r]] · rsqrt(mean(x²) + eps) · w'), w' = 1 + w or w
+// (rowmap NULL: row r itself).
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            _Float16* __restrict__ y,
                                                            const uint32_t* __restrict__ rowmap, uint32_t h,
                                                            uint32_t ld_in, uint32_t ld_out, uint32_t add_one,
                                                            float eps) {
   __shared__ float sh[4];
-  const float* xr = x + (size_t)rowmap[blockIdx.x] * ld_in;
+  const float* xr = x + (size_t)(rowmap ? rowmap[blockIdx.x] : blockIdx.x) * ld_in;
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < h; i += 256) {
     const float v = xr[i];
@@ -154,6 +155,19 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
 // loads in flight together), summed in the lane then across the wave, and
 // written as half4. Four rows per workgroup.
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// One float4's term of a row's sum of squares, and one float4 of the normed
+// row: the arithmetic of every vectorised norm here, so they store the same
+// bits. The pairs' fused multiply-adds are written out: left to the compiler,
+// which product of a pair it fuses differed between kernels.
+__device__ __forceinline__ float sq4(const f4& v) { return fmaf(v[0], v[0], v[1] * v[1]) + fmaf(v[2], v[2], v[3] * v[3]); }
+__device__ __forceinline__ h4 norm4(const f4& v, float inv, const float* __restrict__ w, uint32_t i, uint32_t add_one) {
+  f4 wv = *(const f4*)(w + 4 * i);
+  if (add_one) wv += 1.0f;
+  const f4 o = v * inv * wv;
+  return h4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+}
 
 template <int KV>
 __global__ __launch_bounds__(256) void rmsnorm_rows_vec_kernel(const float* __restrict__ x, const float* __restrict__ w,
@@ -161,11 +175,10 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_vec_kernel(const float* __re
                                                                const uint32_t* __restrict__ rowmap, uint32_t rows,
                                                                uint32_t h, uint32_t ld_in, uint32_t ld_out,
                                                                uint32_t add_one, float eps) {
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const uint32_t lane = threadIdx.x & 63, n4 = h / 4;
-  const float* xr = x + (size_t)rowmap[row] * ld_in;
+  const float* xr = x + (size_t)(rowmap ? rowmap[row] : row) * ld_in;
   f4 v[KV];
 #pragma unroll
   for (int q = 0; q < KV; ++q) {
@@ -174,19 +187,102 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_vec_kernel(const float* __re
   }
   float ss = 0.f;
 #pragma unroll
-  for (int q = 0; q < KV; ++q) ss += (v[q][0] * v[q][0] + v[q][1] * v[q][1]) + (v[q][2] * v[q][2] + v[q][3] * v[q][3]);
+  for (int q = 0; q < KV; ++q) ss += sq4(v[q]);
   const float inv = rsqrtf(wave_sum(ss) / (float)h + eps);
   _Float16* yr = y + (size_t)row * ld_out;
 #pragma unroll
   for (int q = 0; q < KV; ++q) {
     const uint32_t i = lane + 64 * q;
-    if (i < n4) {
-      f4 wv = *(const f4*)(w + 4 * i);
-      if (add_one) wv += 1.0f;
-      const f4 o = v[q] * inv * wv;
-      *(h4*)(yr + 4 * i) = h4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
-    }
+    if (i < n4) *(h4*)(yr + 4 * i) = norm4(v[q], inv, w, i, add_one);
   }
+}
+
+// The residual add of a split-K projection fused with the norm that follows it:
+//   x[r] += Σ_s ws[s][r]   (the partials summed in split order, then added to the row: splitk_reduce_kernel's AddF32)
+//   y[r] = half(x[r] · rsqrt(mean(x[r]²) + eps) · w')   (rmsnorm_rows_vec_kernel<KV>'s arithmetic)
+// One workgroup of 32·KV threads per row, two float4s per thread, every load of the row (S partials and the
+// residual) in flight at once. The sum of squares keeps the vectorised norm's order: each float4's sq4 term goes
+// to LDS, and lane l of wave 0 adds the terms of float4s l, l + 64, ... in that order before the wave sum, so x
+// and y are bitwise those of the reduce followed by the norm.
+template <int KV, int S>
+__global__ __launch_bounds__(32 * KV) void splitk_add_rmsnorm_kernel(const float* __restrict__ ws, uint32_t rows,
+                                                                     uint32_t h, float* __restrict__ x, uint32_t ldx,
+                                                                     const float* __restrict__ w,
+                                                                     _Float16* __restrict__ y, uint32_t ldy,
+                                                                     uint32_t add_one, float eps) {
+  constexpr uint32_t NT = 32 * KV;
+  __shared__ float sq[64 * KV];
+  __shared__ float sinv;
+  const uint32_t row = blockIdx.x, t = threadIdx.x, n4 = h / 4;
+  const size_t plane = (size_t)rows * h;
+  const float* pr = ws + (size_t)row * h;
+  float* xr = x + (size_t)row * ldx;
+  f4 p[S][2], v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t i = t + NT * j;
+#pragma unroll
+    for (int s = 0; s < S; ++s) p[s][j] = i < n4 ? *(const f4*)(pr + s * plane + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
+    v[j] = i < n4 ? *(const f4*)(xr + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t i = t + NT * j;
+    f4 a = p[0][j];
+#pragma unroll
+    for (int s = 1; s < S; ++s) a += p[s][j];
+    v[j] = a + v[j];
+    if (i < n4) *(f4*)(xr + 4 * i) = v[j];
+    sq[i] = i < n4 ? sq4(v[j]) : 0.f;
+  }
+  __syncthreads();
+  if (t < 64) {
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < KV; ++q) ss += sq[t + 64 * q];
+    const float inv = rsqrtf(wave_sum(ss) / (float)h + eps);
+    if (t == 0) sinv = inv;
+  }
+  __syncthreads();
+  const float inv = sinv;
+  _Float16* yr = y + (size_t)row * ldy;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t i = t + NT * j;
+    if (i < n4) *(h4*)(yr + 4 * i) = norm4(v[j], inv, w, i, add_one);
+  }
+}
+
+bool splitk_add_rmsnorm_fits(uint32_t splits, uint32_t h, uint32_t ldx, uint32_t ldy, const void* x, const void* w,
+                             const void* y) {
+  // the rows launch_rmsnorm_rows gives to rmsnorm_rows_vec_kernel<10>
+  return splits >= 2 && splits <= 8 && h % 4 == 0 && h >= 4 && h <= 256 * 10 && ldx % 4 == 0 && ldy % 4 == 0 &&
+         (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)y % 8 == 0;
+}
+
+hipError_t launch_splitk_add_rmsnorm(const float* ws, uint32_t splits, uint32_t rows, uint32_t h, float* x,
+                                     uint32_t ldx, const float* w, _Float16* y, uint32_t ldy, bool add_one, float eps,
+                                     hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  const uint32_t a1 = add_one ? 1u : 0u;
+#define DH_ADDNORM(S_)                                                                                           \
+  case S_:                                                                                                       \
+    hipLaunchKernelGGL((splitk_add_rmsnorm_kernel<10, S_>), dim3(rows), dim3(320), 0, s, ws, rows, h, x, ldx, w, y, \
+                       ldy, a1, eps);                                                                            \
+    break;
+  switch (splits) {
+    DH_ADDNORM(2)
+    DH_ADDNORM(3)
+    DH_ADDNORM(4)
+    DH_ADDNORM(5)
+    DH_ADDNORM(6)
+    DH_ADDNORM(7)
+    DH_ADDNORM(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef DH_ADDNORM
+  return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, _Float16* y, const uint32_t* rowmap, uint32_t rows,

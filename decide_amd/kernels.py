@@ -116,6 +116,14 @@ class Gemm:
         _call(self.lib.dh_gemm_nt(self.ctx.handle, ctypes.c_void_p(stream), addr(x), ldx, addr(w), ldw, addr(y),
                                   ldy, m, n, k, int(epi)))
 
+    def gemm_add_rmsnorm(self, stream: int, x: Arg, w: Arg, y: Arg, m: int, n: int, k: int, ldx: int, ldw: int,
+                         ldy: int, norm_w: Arg, h: Arg, ldh: int, add_one: bool = True, eps: float = 1e-6) -> None:
+        """``y += X · Wᵀ`` (fp32 y, the AddF32 epilogue), then ``h = rmsnorm(y)`` fp16 row by row: bitwise
+        ``gemm(..., AddF32)`` followed by the row norm, one kernel for both where K is split."""
+        _call(self.lib.dh_gemm_add_rmsnorm(self.ctx.handle, ctypes.c_void_p(stream), addr(x), ldx, addr(w), ldw,
+                                           addr(y), ldy, m, n, k, addr(norm_w), 1 if add_one else 0, eps, addr(h),
+                                           ldh))
+
     def gemm_grouped(self, stream: int, x: Arg, ldx: int, m: int, k: int,
                      members: Sequence[Tuple[Arg, int, int, Arg, int, Epilogue]]) -> None:
         """Every member ``(w, ldw, n, y, ldy, epi)`` shares X; one launch."""

@@ -186,6 +186,18 @@ int dh_rmsnorm_rows(dh_ctx* ctx, void* stream, const float* x, const float* w, u
                     const uint32_t* rowmap, uint32_t rows, uint32_t h, uint32_t ld_in, uint32_t ld_out,
                     uint32_t add_one, float eps);
 
+/* --- residual add fused with the norm that follows it (no single counterpart in decide: its forward runs
+ *     the projection with the AddF32 epilogue, then rmsnorm over the same rows, forward.rs:1256-1282 with
+ *     norm.rs:26-33) ---
+ * y += X · Wᵀ (dh_gemm_nt with DH_EPI_ADD_F32, the same contract), then h[r] = half(y[r] * rsqrt(mean(y[r]^2)
+ * + eps) * (add_one ? 1 + w : w)) for r < m (dh_rmsnorm_rows with rows r itself, h = n, ld_in = ldy,
+ * ld_out = ldh). y and h are bitwise those of the two calls. Where the planner splits K, one kernel sums the
+ * partials, adds the residual and norms each row, in place of the split-K reduce and the norm kernel.
+ * Contract: as dh_gemm_nt, plus n >= 32 and n <= ldh. */
+int dh_gemm_add_rmsnorm(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, const void* w, uint32_t ldw, float* y,
+                        uint32_t ldy, uint32_t m, uint32_t n, uint32_t k, const float* norm_w, uint32_t add_one,
+                        float eps, uint16_t* h, uint32_t ldh);
+
 /* --- synthetic inputs (decide: the random-init role of testutil::uniform,
  *     testutil.rs:4-8, with the Gaussian shapes BASELINE asks for) ---
  * Fills n fp16 values with N(0, std) from a counter-based generator keyed by
