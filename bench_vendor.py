@@ -3,7 +3,8 @@
 
 `torch.matmul` on ROCm dispatches fp16 GEMMs to hipBLASLt. This times Y = X·Wᵀ (plain store epilogue: no
 SwiGLU, no residual add) for the shapes decide_amd.shape_report measures with this build's kernels, with
-HIP events over 100 launches after 20 warm-ups. The kernel each shape runs, and its own duration, come from
+HIP events over 100 launches after 20 warm-ups; for the gate|up shapes also the product followed by the SwiGLU
+decide's path takes from it (eager torch: fp32 silu(gate)·up over the 16-column interleave, rounded to fp16). The kernel each shape runs, and its own duration, come from
 running this module under the profiler:
 
     rocprofv3 --kernel-trace --stats -d gpurun_out/blas -o mm --output-format csv -- python3 bench_vendor.py
@@ -40,8 +41,25 @@ def main() -> None:
         e1.record()
         e1.synchronize()
         us = e0.elapsed_time(e1) / 100 * 1e3
-        print(json.dumps({"shape": name, "m": m, "n": n, "k": k, "event_us": round(us, 2),
-                          "tflops": round(2.0 * m * n * k / us / 1e6, 1)}), flush=True)
+        rec = {"shape": name, "m": m, "n": n, "k": k, "event_us": round(us, 2),
+               "tflops": round(2.0 * m * n * k / us / 1e6, 1)}
+        if "gate|up" in name:
+            # what decide's path needs from this product: silu(gate) * up over the 16-column interleave, in fp32,
+            # rounded to fp16 (this build fuses it into the GEMM's epilogue; here it is eager torch after it)
+            def swiglu(y):
+                v = y.view(m, n // 32, 2, 16).float()
+                return (torch.nn.functional.silu(v[:, :, 0]) * v[:, :, 1]).half()
+            for _ in range(5):
+                o = swiglu(x @ w.t())
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(50):
+                o = swiglu(x @ w.t())
+            e1.record()
+            e1.synchronize()
+            rec["with_swiglu_event_us"] = round(e0.elapsed_time(e1) / 50 * 1e3, 2)
+            del o
+        print(json.dumps(rec), flush=True)
         del y
 
 
