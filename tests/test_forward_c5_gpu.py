@@ -5,7 +5,8 @@ The oracle forward (tests/oracle_forward.py: cpu_ref.rs pieces with decide's rou
 runs at the extremes the CPU can finish in well under a minute each:
   * length: 4 layers at T = 2,307 (the chunked recurrence over 2,307 steps and 2,307-key causal attention over every
     row, no pruning), bar 0.01;
-  * depth: 24 layers at T = 256, bar 0.01, and all 36 layers at T = 256 (the last one pruned to 3 answer rows).
+  * depth: 24 layers at T = 256, bar 0.01, and all 36 layers at T = 256 (the last one pruned to 3 answer rows);
+  * 8 layers at T = 603, the shorter prompt length BASELINE reports, bar 0.01.
 At 36 layers this random-init model amplifies fp32-level differences to about the size of the bar itself: the same
 oracle with its GEMM sums in fp32 (orc_gemm_f32_fast) instead of f64 differs from the f64 oracle by 0.006-0.013 in
 max |Δlogit| over six seed/init choices, and the GPU forward by 0.007-0.011. So the 36-layer test computes that
@@ -104,6 +105,13 @@ def test_forward_matches_oracle_at_length(gpu, kernels):
 def test_forward_matches_oracle_at_depth(gpu, kernels):
     """24 layers (18 Gated-DeltaNet, 6 gated attention; the last one pruned) at T = 256."""
     diff, _ = _oracle_drift(kernels, 24, 256, True, seed=5100)
+    assert diff <= MAX_LOGIT_DIFF, f"max |Δlogit| {diff:.4g}"
+
+
+def test_forward_matches_oracle_at_603_tokens(gpu, kernels):
+    """8 layers (6 Gated-DeltaNet, 2 gated attention) at BASELINE's shorter prompt length, where the residual
+    projections split K and their partials meet the residual and the next norm in one kernel."""
+    diff, _ = _oracle_drift(kernels, 8, 603, True, seed=5400)
     assert diff <= MAX_LOGIT_DIFF, f"max |Δlogit| {diff:.4g}"
 
 
