@@ -162,11 +162,17 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 // bits. The pairs' fused multiply-adds are written out: left to the compiler,
 // which product of a pair it fuses differed between kernels.
 __device__ __forceinline__ float sq4(const f4& v) { return fmaf(v[0], v[0], v[1] * v[1]) + fmaf(v[2], v[2], v[3] * v[3]); }
-__device__ __forceinline__ h4 norm4(const f4& v, float inv, const float* __restrict__ w, uint32_t i, uint32_t add_one) {
+__device__ __forceinline__ f4 weight4(const float* __restrict__ w, uint32_t i, uint32_t add_one) {
   f4 wv = *(const f4*)(w + 4 * i);
   if (add_one) wv += 1.0f;
+  return wv;
+}
+__device__ __forceinline__ h4 norm4w(const f4& v, float inv, const f4& wv) {
   const f4 o = v * inv * wv;
   return h4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+}
+__device__ __forceinline__ h4 norm4(const f4& v, float inv, const float* __restrict__ w, uint32_t i, uint32_t add_one) {
+  return norm4w(v, inv, weight4(w, i, add_one));
 }
 
 template <int KV>
@@ -217,13 +223,14 @@ __global__ __launch_bounds__(32 * KV) void splitk_add_rmsnorm_kernel(const float
   const size_t plane = (size_t)rows * h;
   const float* pr = ws + (size_t)row * h;
   float* xr = x + (size_t)row * ldx;
-  f4 p[S][2], v[2];
+  f4 p[S][2], v[2], wv[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const uint32_t i = t + NT * j;
 #pragma unroll
     for (int s = 0; s < S; ++s) p[s][j] = i < n4 ? *(const f4*)(pr + s * plane + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
     v[j] = i < n4 ? *(const f4*)(xr + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
+    wv[j] = i < n4 ? weight4(w, i, add_one) : f4{0.f, 0.f, 0.f, 0.f};  // with the row: no load after the barriers
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(32 * KV) void splitk_add_rmsnorm_kernel(const float
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const uint32_t i = t + NT * j;
-    if (i < n4) *(h4*)(yr + 4 * i) = norm4(v[j], inv, w, i, add_one);
+    if (i < n4) *(h4*)(yr + 4 * i) = norm4w(v[j], inv, wv[j]);
   }
 }
 
