@@ -150,10 +150,11 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
   }
 }
 
-// The same norm with one wave per row for 16-byte-aligned rows of h % 4 == 0,
-// h <= 256·KV: the row is loaded once into registers (KV float4 per lane, all
-// loads in flight together), summed in the lane then across the wave, and
-// written as half4. Four rows per workgroup.
+// The same norm with one wave per two rows for 16-byte-aligned rows of
+// h % 4 == 0, h <= 256·KV: each row is loaded once into registers (KV float4
+// per lane, all loads of both rows and of the weights in flight together),
+// summed in the lane then across the wave, and written as half4. Eight rows
+// per workgroup.
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
@@ -181,25 +182,38 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_vec_kernel(const float* __re
                                                                const uint32_t* __restrict__ rowmap, uint32_t rows,
                                                                uint32_t h, uint32_t ld_in, uint32_t ld_out,
                                                                uint32_t add_one, float eps) {
-  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  // two rows per wave: the weights are loaded once for both, and both rows' loads are in flight together
+  const uint32_t row0 = 2 * (blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (row0 >= rows) return;
   const uint32_t lane = threadIdx.x & 63, n4 = h / 4;
-  const float* xr = x + (size_t)(rowmap ? rowmap[row] : row) * ld_in;
-  f4 v[KV];
+  const bool two = row0 + 1 < rows;
+  const float* xr0 = x + (size_t)(rowmap ? rowmap[row0] : row0) * ld_in;
+  const float* xr1 = two ? x + (size_t)(rowmap ? rowmap[row0 + 1] : row0 + 1) * ld_in : xr0;
+  f4 v0[KV], v1[KV], wv[KV];
 #pragma unroll
   for (int q = 0; q < KV; ++q) {
     const uint32_t i = lane + 64 * q;
-    v[q] = i < n4 ? *(const f4*)(xr + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
+    v0[q] = i < n4 ? *(const f4*)(xr0 + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
+    v1[q] = i < n4 ? *(const f4*)(xr1 + 4 * i) : f4{0.f, 0.f, 0.f, 0.f};
+    wv[q] = i < n4 ? weight4(w, i, add_one) : f4{0.f, 0.f, 0.f, 0.f};
   }
-  float ss = 0.f;
+  float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
-  for (int q = 0; q < KV; ++q) ss += sq4(v[q]);
-  const float inv = rsqrtf(wave_sum(ss) / (float)h + eps);
-  _Float16* yr = y + (size_t)row * ld_out;
+  for (int q = 0; q < KV; ++q) {
+    ss0 += sq4(v0[q]);
+    ss1 += sq4(v1[q]);
+  }
+  const float inv0 = rsqrtf(wave_sum(ss0) / (float)h + eps);
+  const float inv1 = rsqrtf(wave_sum(ss1) / (float)h + eps);
+  _Float16* yr0 = y + (size_t)row0 * ld_out;
+  _Float16* yr1 = yr0 + ld_out;
 #pragma unroll
   for (int q = 0; q < KV; ++q) {
     const uint32_t i = lane + 64 * q;
-    if (i < n4) *(h4*)(yr + 4 * i) = norm4(v[q], inv, w, i, add_one);
+    if (i < n4) {
+      *(h4*)(yr0 + 4 * i) = norm4w(v0[q], inv0, wv[q]);
+      if (two) *(h4*)(yr1 + 4 * i) = norm4w(v1[q], inv1, wv[q]);
+    }
   }
 }
 
@@ -298,7 +312,7 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, _Float16* y, cons
   const bool vec = h % 4 == 0 && h <= 256 * 16 && ld_in % 4 == 0 && ld_out % 4 == 0 && (uintptr_t)x % 16 == 0 &&
                    (uintptr_t)w % 16 == 0 && (uintptr_t)y % 8 == 0;
   if (vec) {
-    const dim3 grid((rows + 3) / 4);
+    const dim3 grid((rows + 7) / 8);
     if (h <= 256 * 10)
       hipLaunchKernelGGL(rmsnorm_rows_vec_kernel<10>, grid, dim3(256), 0, s, x, w, y, rowmap, rows, h, ld_in, ld_out,
                          add_one ? 1u : 0u, eps);
