@@ -914,11 +914,15 @@ struct Pipe8 {
   }
 };
 
-// Epilogue of the 8-wave tile, through LDS in fp32 (row stride 292 floats):
+// Epilogue of the 8-wave tile, through LDS in fp32 (row stride BN + 4 floats):
 // 64 rows at a time, each wave writes its fragments of those rows, then all
 // 512 threads store whole rows with 16-byte stores (SwiGLU reads each
 // 8-column output chunk's gate and up halves back from the staged rows).
-template <int FM, int FN, int BN>
+// PAIRS (both halves' fragment counts even, so every wave's first column is
+// a multiple of 32 and it holds whole gate|up pairs): SwiGLU runs in
+// registers and the fp16 tile goes through LDS once, the same values with a
+// quarter of the barriers and half the LDS bytes.
+template <int FM, int FN, int BN, bool PAIRS>
 __device__ __forceinline__ void store_tile8(f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split, uint32_t m0,
                                             uint32_t n0, int rbase, int cbase, int r, int g, float* stage) {
   constexpr int LDR = BN + 4, CR = 64, NT = 512, BM = 32 * FM;
@@ -929,6 +933,44 @@ __device__ __forceinline__ void store_tile8(f4 (&acc)[FM][FN], const TileArgs& p
   const bool partial = p.splits > 1;
   const uint32_t esz = (partial || epi == 0u || epi == 2u) ? 4u : 2u;
   const bool vec16 = partial || ((((uintptr_t)Y) % 16) == 0 && ((size_t)ldy * esz) % 16 == 0);
+  if constexpr (PAIRS) {
+    if (epi == 3u && !partial) {
+      constexpr int OW = BN / 2, LDH = OW + 8, OQ = OW / 8;  // fp16 row stride (halves), 16-byte chunks per row
+      static_assert(FN % 2 == 0, "whole gate|up pairs per wave");
+      _Float16* st = (_Float16*)stage;
+      __syncthreads();  // every wave is past its main-loop LDS reads
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; j += 2) {
+          pin_acc(acc[i][j]);
+          pin_acc(acc[i][j + 1]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            st[(rbase + 16 * i + 4 * g + e) * LDH + cbase / 2 + (j / 2) * 16 + r] =
+                (_Float16)swiglu_f(acc[i][j][e], acc[i][j + 1][e]);
+        }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < (BM * OQ + NT - 1) / NT; ++it) {
+        const int item = it * NT + tid;
+        if (item >= BM * OQ) break;
+        const int row = item / OQ, oq = item % OQ;
+        const uint32_t grow = m0 + row;
+        if (grow >= M || n0 + 32 * (oq / 2) >= N) continue;
+        const h8 o = *(const h8*)(st + row * LDH + oq * 8);
+        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + (n0 / 2) + oq * 8;
+        if (vec16) {
+          __builtin_nontemporal_store(o, (h8*)dst);
+        } else {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) *(h2*)(dst + e) = h2{o[e], o[e + 1]};
+        }
+      }
+      return;
+    }
+  }
   static_for<0, (BM + CR - 1) / CR>([&](auto cc) {
     constexpr int c0 = decltype(cc)::value * CR;
     constexpr int rows = (BM - c0) < CR ? (BM - c0) : CR;
@@ -1112,7 +1154,7 @@ __device__ __forceinline__ void tile8_wave(const TileArgs& p, char* lds, int wav
     });
   }
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  store_tile8<FM, FN, BN>(pp.acc, p, mi, split, m0, n0, rbase, cbase, r, g, (float*)lds);
+  store_tile8<FM, FN, BN, FNA % 2 == 0 && FNB % 2 == 0>(pp.acc, p, mi, split, m0, n0, rbase, cbase, r, g, (float*)lds);
 }
 
 template <int FM, int FNA, int FNB>
@@ -1122,6 +1164,7 @@ void gemm_tile8_kernel(const TileArgs p) {
   constexpr int LDSB = 2 * BM * 128 + 3 * BN * 128;
   static_assert(LDSB <= 160 * 1024, "the rings fit the LDS");
   static_assert(LDSB >= 64 * (BN + 4) * 4, "the epilogue's staging fits the rings");
+  static_assert(LDSB >= BM * (BN / 2 + 8) * 2, "the fp16 SwiGLU staging fits the rings");
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
   const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t mt = wid % p.mtiles;
