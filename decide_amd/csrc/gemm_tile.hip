@@ -915,7 +915,7 @@ struct Pipe8 {
 };
 
 // Epilogue of the 8-wave tile, through LDS in fp32 (row stride BN + 4 floats):
-// 64 rows at a time, each wave writes its fragments of those rows, then all
+// 128 rows at a time, each wave writes its fragments of those rows, then all
 // 512 threads store whole rows with 16-byte stores (SwiGLU reads each
 // 8-column output chunk's gate and up halves back from the staged rows).
 // PAIRS (both halves' fragment counts even, so every wave's first column is
@@ -925,7 +925,7 @@ struct Pipe8 {
 template <int FM, int FN, int BN, bool PAIRS>
 __device__ __forceinline__ void store_tile8(f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split, uint32_t m0,
                                             uint32_t n0, int rbase, int cbase, int r, int g, float* stage) {
-  constexpr int LDR = BN + 4, CR = 64, NT = 512, BM = 32 * FM;
+  constexpr int LDR = BN + 4, CR = 128, NT = 512, BM = 32 * FM;
   const uint32_t M = p.m, N = p.mem[mi].n;
   const int tid = threadIdx.x;
   const uint32_t epi = p.mem[mi].epi, ldy = p.mem[mi].ldy;
@@ -1163,7 +1163,7 @@ void gemm_tile8_kernel(const TileArgs p) {
   constexpr int BN = 32 * (FNA + FNB), BM = 32 * FM;
   constexpr int LDSB = 2 * BM * 128 + 3 * BN * 128;
   static_assert(LDSB <= 160 * 1024, "the rings fit the LDS");
-  static_assert(LDSB >= 64 * (BN + 4) * 4, "the epilogue's staging fits the rings");
+  static_assert(LDSB >= 128 * (BN + 4) * 4, "the epilogue's staging fits the rings");
   static_assert(LDSB >= BM * (BN / 2 + 8) * 2, "the fp16 SwiGLU staging fits the rings");
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
   const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
