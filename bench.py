@@ -17,7 +17,8 @@ timed with HIP events on the stream it runs on (one step in four), against 2.5 P
 fp16 MFMA. `cpu_baseline` times the whole block on the host's cores with the
 oracle's blocked fp32 GEMM, and beside it decide's cpu_ref::gemm_nt restated in
 C (f64 sums, single thread) on a bounded sample of rows. The config-5 forward
-(36 layers at 2,307 and 603 tokens) is timed first; see forward_timing.
+(36 layers at 2,307 and 603 tokens) is timed first, then decide's own model and
+requests on its snapshot route; see forward_timing and reference_forward_timing.
 """
 
 from __future__ import annotations
@@ -245,6 +246,58 @@ def forward_timing(k, runs: int, with_graph: bool = True):
                       "3 answers x 8 candidates, random-init", "runs": runs, "tokens": out}, model
 
 
+def reference_forward_timing(k, runs: int):
+    """decide's own model and requests (config.rs:5, 32, 36; README.md:17-20): 32 layers, vocab 248,320, the
+    snapshot route after a 107-token prefix, in chunks of decide's CHUNK = 512 rows and in this library's default
+    of one chunk per request, card (276 tokens, 3 answers),
+    ticket (603 tokens, 6 answers) and long-document (2,307 tokens, 3 answers) requests with 2..62 candidates per
+    answer, random-init weights. Each request is one dh_model_logits call, which stages the host ids, runs the
+    forward and returns the host logits (decide's "forward" span, bench.rs:40-47), timed on the host clock:
+    p50 of `runs` after 3 warm-ups."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from make_forward_logits import REF_MAX_CAND, REF_PREFIX, REF_VOCAB, request_ref
+
+    from decide_amd.forward import Model, ModelConfig
+    from decide_amd.hip import Stream
+
+    cfg = ModelConfig(layers=32, vocab=REF_VOCAB, max_tokens=2307, max_answers=16, max_cand=REF_MAX_CAND)
+    st = Stream()
+    s = st.handle
+    model = Model(k.ctx, cfg)
+    model.init_random(s, seed=0xDEC1DE)
+    k.gemm.warm_up(s, max_m=512)
+    model.set_chunk(512)
+    prefix = request_ref(276, 3)[0][:REF_PREFIX]
+    model.build_snapshot(s, [int(v) for v in prefix])
+    out = {}
+    for name, (t, n_ans) in (("card", (276, 3)), ("ticket", (603, 6)), ("long", (2307, 3))):
+        ids, ans, cand, ncand = request_ref(t, n_ans)
+        ids = [int(v) for v in ids]
+        answers = [(int(r), [int(c) for c in cand[i, :ncand[i]]]) for i, r in enumerate(ans)]
+        rec = {"tokens": t, "answers": n_ans, "rows_computed": t - REF_PREFIX}
+        # decide's CHUNK = 512 rows (config.rs:36), then this library's default: the whole span in one chunk
+        for key, chunk in (("chunk512", 512), ("one_chunk", cfg.max_tokens)):
+            model.set_chunk(chunk)
+            for _ in range(3):
+                lg = model.logits(s, ids, answers)
+            assert model.last_route() == "snapshot" and model.last_start() == REF_PREFIX
+            times = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                lg = model.logits(s, ids, answers)
+                times.append((time.perf_counter() - t0) * 1e3)
+            assert all(np.isfinite(row).all() for row in lg)
+            rec[f"p50_ms_{key}"] = round(float(np.percentile(times, 50)), 3)
+        out[name] = rec
+    model.close()
+    st.destroy()
+    return {"config": "decide's model shape: 32 layers (24 GDN + 8 gated attention), vocab 248320, snapshot route "
+                      "after a 107-token prefix, 2..62 candidates per answer, random-init; chunks of 512 rows "
+                      "(decide's CHUNK) and the whole span in one chunk (this library's default)",
+            "runs": runs, "requests": out,
+            "reference_m1pro_gpu_only_p50_ms": {"card": 342, "ticket": 922, "long": 5260}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -286,6 +339,8 @@ def main():
     # run up to 20 % slower than the settled state), so the C2 warm-up follows it with no idle gap; the model is
     # released only after the C2 timing for the same reason.
     fwd, fwd_model = forward_timing(k, args.forward_runs, not args.no_graph) if not args.no_forward else (None, None)
+    if fwd is not None:
+        fwd["reference_shape"] = reference_forward_timing(k, args.forward_runs)
     base_loaded = k.gemm.fast_pipelines()
 
     def step(i, ev=None):

@@ -4,7 +4,10 @@
 `torch.matmul` on ROCm dispatches fp16 GEMMs to hipBLASLt. This times Y = X·Wᵀ (plain store epilogue: no
 SwiGLU, no residual add) for the shapes decide_amd.shape_report measures with this build's kernels, with
 HIP events over 100 launches after 20 warm-ups; for the gate|up shapes also the product followed by the SwiGLU
-decide's path takes from it (eager torch: fp32 silu(gate)·up over the 16-column interleave, rounded to fp16). The kernel each shape runs, and its own duration, come from
+decide's path takes from it (eager torch: fp32 silu(gate)·up over the 16-column interleave, rounded to fp16).
+Interleaved with each (same box, same tensors, same stream), this build's planned kernel for the shape with the
+epilogue decide's path runs (C1 StoreF32, gate|up SwiGLU, down the residual add), by the same events: two rounds
+per shape, reported as `this_build_event_us`. The kernel each shape runs, and its own duration, come from
 running this module under the profiler:
 
     rocprofv3 --kernel-trace --stats -d gpurun_out/blas -o mm --output-format csv -- python3 bench_vendor.py
@@ -22,11 +25,40 @@ SHAPES = [  # (name, M, N, K) — BASELINE's C1, the C2 MLP pair and the C4 gate
 ]
 
 
+def _this_build(kernels, x, w, name: str, m: int, n: int, k: int, launches: int = 100) -> float:
+    """Mean µs per launch of this build's planned kernel on the same tensors, with the path's epilogue."""
+    import torch
+
+    from decide_amd.kernels import Epilogue
+
+    epi = Epilogue.SwigluF16 if "gate|up" in name else Epilogue.AddF32 if "down" in name else Epilogue.StoreF32
+    cols = n // 2 if epi == Epilogue.SwigluF16 else n
+    y = torch.zeros(m, cols, device="cuda", dtype=torch.float16 if epi == Epilogue.SwigluF16 else torch.float32)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        kernels.gemm.gemm(s, (x, 0), (w, 0), (y, 0), m, n, k, k, k, cols, epi)
+
+    for _ in range(20):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(launches):
+        run()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / launches * 1e3
+
+
 def main() -> None:
     import torch
 
     if not torch.cuda.is_available():
         raise SystemExit("no GPU")
+    from decide_amd.kernels import Kernels
+
+    kernels = Kernels()
     torch.manual_seed(0)
     for name, m, n, k in SHAPES:
         x = torch.randn(m, k, device="cuda", dtype=torch.float16)
@@ -59,6 +91,16 @@ def main() -> None:
             e1.synchronize()
             rec["with_swiglu_event_us"] = round(e0.elapsed_time(e1) / 50 * 1e3, 2)
             del o
+        # interleaved: this build, the library again, this build again
+        ours = [_this_build(kernels, x, w, name, m, n, k)]
+        e0.record()
+        for _ in range(100):
+            y = x @ w.t()
+        e1.record()
+        e1.synchronize()
+        rec["event_us_second_round"] = round(e0.elapsed_time(e1) / 100 * 1e3, 2)
+        ours.append(_this_build(kernels, x, w, name, m, n, k))
+        rec["this_build_event_us"] = [round(v, 2) for v in ours]
         print(json.dumps(rec), flush=True)
         del y
 

@@ -50,30 +50,69 @@ void mark(dh_ctx* c, int kid) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+bool forced_plan(const dh_ctx* c, int* variant, uint32_t* splits) {
+  const uint64_t f = c ? c->forced.load(std::memory_order_relaxed) : ~0ull;
+  if (f == ~0ull) return false;
+  *variant = (int)(uint32_t)f;
+  *splits = (uint32_t)(f >> 32);
+  return true;
+}
+
 namespace {
-// Grows *buf to at least `bytes` (by at least half its size, so a run of small
-// growths retires little); the old buffer joins c->retired.
-int grow(dh_ctx* c, float** buf, uint64_t* have, uint64_t bytes, uint64_t cap, const char* what) {
+// Grows one of `stream`'s workspaces (`aux` selects which) to at least `bytes`:
+// by at least half its size, so a run of small growths retires little, or
+// exactly `bytes` when the larger request fails. The old buffer joins
+// c->retired.
+int grow(dh_ctx* c, hipStream_t stream, bool aux, uint64_t bytes, uint64_t cap, const char* what, float** out) {
   std::lock_guard<std::mutex> g(c->ws_lock);
-  if (bytes <= *have) return DH_OK;
+  dh_stream_ws* sw = nullptr;
+  for (dh_stream_ws& e : c->streams)
+    if (e.stream == stream) sw = &e;
+  if (!sw) {
+    c->streams.push_back(dh_stream_ws{});
+    sw = &c->streams.back();
+    sw->stream = stream;
+  }
+  float** buf = aux ? &sw->aux : &sw->ws;
+  uint64_t* have = aux ? &sw->aux_bytes : &sw->ws_bytes;
+  if (bytes <= *have) {
+    *out = *buf;
+    return DH_OK;
+  }
   if (bytes > cap)
     return fail(DH_ENOMEM, "%s of %llu bytes exceeds its %llu-byte ceiling", what, (unsigned long long)bytes,
                 (unsigned long long)cap);
-  const uint64_t want = std::min(cap, std::max(bytes, *have + *have / 2));
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(DH_EINVAL,
+                "%s must grow to %llu bytes on a stream that is being captured; size it first with dh_warm_up "
+                "or an eager call of the same size on this stream",
+                what, (unsigned long long)bytes);
+  uint64_t want = std::min(cap, std::max(bytes, *have + *have / 2));
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, want);
+  if (e != hipSuccess && want > bytes) {
+    (void)hipGetLastError();
+    want = bytes;
+    e = hipMalloc(&p, want);
+  }
   if (e != hipSuccess)
     return fail(DH_ENOMEM, "%s of %llu bytes: %s", what, (unsigned long long)want, hipGetErrorString(e));
   if (*buf) c->retired.push_back(*buf);
   *buf = (float*)p;
   *have = want;
+  *out = *buf;
   return DH_OK;
 }
 }  // namespace
 
-int ensure_aux(dh_ctx* c, uint64_t bytes) { return grow(c, &c->aux, &c->aux_bytes, bytes, UINT64_MAX, "forward workspace"); }
+int ensure_aux(dh_ctx* c, hipStream_t stream, uint64_t bytes, float** out) {
+  return grow(c, stream, true, bytes, UINT64_MAX, "forward workspace", out);
+}
 
-int ensure_ws(dh_ctx* c, uint64_t bytes) { return grow(c, &c->ws, &c->ws_bytes, bytes, c->ws_cap, "split-K workspace"); }
+int ensure_ws(dh_ctx* c, hipStream_t stream, uint64_t bytes, float** out) {
+  return grow(c, stream, false, bytes, c->ws_cap, "split-K workspace", out);
+}
 
 }  // namespace dh_api
 
@@ -134,9 +173,9 @@ int check_gemm(const dh_ctx* c, const void* x, uint32_t ldx, const void* w, uint
 }
 
 dh::Plan choose_plan(const dh_ctx* c, uint32_t m, uint32_t n, uint32_t k, uint32_t epi) {
-  if (c && c->forced_variant >= 0) {
-    return dh::plan_make(c->forced_variant, std::max(1u, c->forced_splits), m, n, k, epi);
-  }
+  int fv;
+  uint32_t fs;
+  if (forced_plan(c, &fv, &fs)) return dh::plan_make(fv, std::max(1u, fs), m, n, k, epi);
   return dh::plan_gemm(m, n, k, epi, c ? c->ws_cap : (512ull << 20));
 }
 
@@ -181,9 +220,8 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
     if (fixed_ws) {
       a.ws = fixed_ws;
     } else {
-      int rc = ensure_ws(c, p.ws_bytes);
+      int rc = ensure_ws(c, s, p.ws_bytes, &a.ws);
       if (rc != DH_OK) return rc;
-      a.ws = c->ws;
     }
   }
   int rc;
@@ -242,8 +280,10 @@ int dh_ctx_create(uint32_t flags, dh_ctx** out) {
 
 void dh_ctx_destroy(dh_ctx* ctx) {
   if (!ctx) return;
-  if (ctx->ws) (void)hipFree(ctx->ws);
-  if (ctx->aux) (void)hipFree(ctx->aux);
+  for (const dh_stream_ws& e : ctx->streams) {
+    if (e.ws) (void)hipFree(e.ws);
+    if (e.aux) (void)hipFree(e.aux);
+  }
   for (void* p : ctx->retired) (void)hipFree(p);
   delete ctx;
 }
@@ -319,9 +359,10 @@ int dh_gemm_nt_noalloc(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, c
                                                 epi, s),
                       "gemm reference kernel launch");
   }
-  const dh::Plan p = ctx->forced_variant >= 0
-                         ? dh::plan_make(ctx->forced_variant, std::max(1u, ctx->forced_splits), m, n, k, epi)
-                         : dh::plan_gemm(m, n, k, epi, dh::kNoAllocScratchBytes);
+  int fv;
+  uint32_t fs;
+  const dh::Plan p = forced_plan(ctx, &fv, &fs) ? dh::plan_make(fv, std::max(1u, fs), m, n, k, epi)
+                                                : dh::plan_gemm(m, n, k, epi, dh::kNoAllocScratchBytes);
   if (p.variant < 0) return fail(DH_EINVAL, "gemm (no-alloc): no plan for M = %u, N = %u, K = %u", m, n, k);
   if (p.ws_bytes > dh::kNoAllocScratchBytes)
     return fail(DH_EINVAL,
@@ -361,8 +402,9 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
     }
     return ok();
   }
-  dh::Plan p = ctx->forced_variant >= 0 ? dh::plan_make(ctx->forced_variant, 1, m, n_total, k, 0u)
-                                        : dh::plan_grouped(m, k, ns, count);
+  int fv;
+  uint32_t fs;
+  dh::Plan p = forced_plan(ctx, &fv, &fs) ? dh::plan_make(fv, 1, m, n_total, k, 0u) : dh::plan_grouped(m, k, ns, count);
   if (p.variant < 0) return fail(DH_EINVAL, "gemm grouped: no plan");
   return launch_plan(ctx, s, p, x, ldx, m, k, members, count);
 }
@@ -394,6 +436,8 @@ int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint
 int dh_gemm_ws_need(const dh_ctx* ctx, uint32_t max_m, uint32_t n, uint32_t k, uint64_t* out) {
   if (!out) return fail(DH_EINVAL, "dh_gemm_ws_need: out is NULL");
   if (max_m < 1 || n % 32 || k % 32) return fail(DH_EINVAL, "dh_gemm_ws_need: invalid shape");
+  if (max_m > DH_PLAN_MAX_ROWS)
+    return fail(DH_EINVAL, "dh_gemm_ws_need: max_m = %u exceeds %u (DH_PLAN_MAX_ROWS)", max_m, DH_PLAN_MAX_ROWS);
   *out = dh::plan_ws_need(max_m, n, k, ctx ? ctx->ws_cap : (512ull << 20));
   return ok();
 }
@@ -401,15 +445,13 @@ int dh_gemm_ws_need(const dh_ctx* ctx, uint32_t max_m, uint32_t n, uint32_t k, u
 int dh_gemm_force(dh_ctx* ctx, uint32_t variant, uint32_t splits) {
   if (!ctx) return fail(DH_EINVAL, "dh_gemm_force: null context");
   if (variant == UINT32_MAX) {
-    ctx->forced_variant = -1;
-    ctx->forced_splits = 0;
+    ctx->forced.store(~0ull, std::memory_order_relaxed);
     return ok();
   }
   if (variant >= (uint32_t)dh::variant_count())
     return fail(DH_EINVAL, "dh_gemm_force: variant %u >= %d", variant, dh::variant_count());
   if (splits < 1 || splits > 64) return fail(DH_EINVAL, "dh_gemm_force: splits = %u must be in 1..64", splits);
-  ctx->forced_variant = (int)variant;
-  ctx->forced_splits = splits;
+  ctx->forced.store((uint64_t)splits << 32 | variant, std::memory_order_relaxed);
   return ok();
 }
 
@@ -427,16 +469,21 @@ int dh_gemm_variant_info(uint32_t variant, uint32_t* bm, uint32_t* bn, uint32_t*
 
 int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
   if (!ctx) return fail(DH_EINVAL, "dh_warm_up: null context");
+  if (max_m > DH_PLAN_MAX_ROWS)
+    return fail(DH_EINVAL, "dh_warm_up: max_m = %u exceeds %u (DH_PLAN_MAX_ROWS)", max_m, DH_PLAN_MAX_ROWS);
   hipStream_t s = (hipStream_t)stream;
   // Size the workspace for the largest split-K plan of decide's engine shapes
   // (gemm_configs.rs:385) at any M up to max_m rows, so no such call grows it.
   static const uint32_t kShapes[][2] = {{2560, 12352}, {2560, 10240}, {2560, 18432}, {4096, 2560},
                                         {9216, 2560},  {2560, 2048},  {2560, 8192},  {2560, 6144}};
   uint64_t need = 0;
-  if (ctx->forced_variant < 0 && !(ctx->flags & DH_GEMM_REFERENCE))
+  int fv;
+  uint32_t fs;
+  if (!forced_plan(ctx, &fv, &fs) && !(ctx->flags & DH_GEMM_REFERENCE))
     for (auto& kn : kShapes) need = std::max(need, dh::plan_ws_need(std::max(1u, max_m), kn[1], kn[0], ctx->ws_cap));
+  float* unused = nullptr;
   if (need) {
-    int rc = ensure_ws(ctx, need);
+    int rc = ensure_ws(ctx, s, need, &unused);
     if (rc != DH_OK) return rc;
   }
   const bool chunked = (ctx->flags & DH_DELTA_CHUNKED) ||
@@ -445,7 +492,7 @@ int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m) {
   uint64_t aux = dh::attention_ws_max(max_m);
   if (chunked) aux = std::max<uint64_t>(aux, dh::delta_chunk_ws_floats(std::max(1u, max_m)) * sizeof(float));
   if (aux) {
-    int rc = ensure_aux(ctx, aux);
+    int rc = ensure_aux(ctx, s, aux, &unused);
     if (rc != DH_OK) return rc;
   }
   // One tiny launch of every tile variant (M = 16, N = bn, K = 64) and of the

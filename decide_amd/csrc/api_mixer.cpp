@@ -30,14 +30,15 @@ int attention_run(dh_ctx* ctx, void* stream, const uint16_t* q, const uint16_t* 
   if (!q || !kc || !vc || !pq || !qpos || !y) return fail(DH_EINVAL, "attention: null pointer");
   const dh::AttnSplit sp = dh::attention_split(rows, npos, ctx->cus);
   const uint64_t ws = dh::attention_ws_bytes(rows, sp);
-  if (ws) {  // allocates only past what dh_warm_up sized the workspace for
-    const int rc = ensure_aux(ctx, ws);
+  float* aux = nullptr;
+  if (ws) {  // allocates only past what dh_warm_up (or an earlier call) sized this stream's workspace for
+    const int rc = ensure_aux(ctx, (hipStream_t)stream, ws, &aux);
     if (rc != DH_OK) return rc;
     mark(ctx, kKidAttnCombine);
   }
   mark(ctx, kKidAttn);
   return hip_status(dh::launch_attention((const _Float16*)q, (const _Float16*)kc, (const _Float16*)vc, pq, qpos,
-                                         (_Float16*)y, ws ? ctx->aux : nullptr, rows, ldq, sp, (hipStream_t)stream),
+                                         (_Float16*)y, aux, rows, ldq, sp, (hipStream_t)stream),
                     "attention");
 }
 
@@ -101,11 +102,12 @@ int dh_gated_delta(dh_ctx* ctx, void* stream, const float* q, const float* k, co
                                              write_state != 0, (hipStream_t)stream),
                       "gated_delta");
   }
-  // allocates only when T exceeds what dh_warm_up sized the workspace for
-  const int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(t) * sizeof(float));
+  // allocates only when T exceeds what dh_warm_up (or an earlier call) sized this stream's workspace for
+  float* aux = nullptr;
+  const int rc = ensure_aux(ctx, (hipStream_t)stream, dh::delta_chunk_ws_floats(t) * sizeof(float), &aux);
   if (rc != DH_OK) return rc;
   mark(ctx, kKidDeltaChunk);
-  return hip_status(dh::launch_gated_delta_chunked(q, k, v, a, b, a_log, dt_bias, state_in, state_out, o, ctx->aux, t,
+  return hip_status(dh::launch_gated_delta_chunked(q, k, v, a, b, a_log, dt_bias, state_in, state_out, o, aux, t,
                                                    ldab, write_state != 0, (hipStream_t)stream),
                     "gated_delta (chunked)");
 }
@@ -128,12 +130,13 @@ int dh_conv_gated_delta_chunked(dh_ctx* ctx, void* stream, const float* p, const
       misaligned(state_out, 16))
     return fail(DH_EINVAL, "conv_delta: p and prev must be 8-byte, w, q and the states 16-byte aligned");
   if (!ctx) return fail(DH_EINVAL, "conv_delta: null context");
-  // allocates only when T exceeds what dh_warm_up sized the workspace for
-  const int rc = ensure_aux(ctx, dh::delta_chunk_ws_floats(t) * sizeof(float));
+  // allocates only when T exceeds what dh_warm_up (or an earlier call) sized this stream's workspace for
+  float* aux = nullptr;
+  const int rc = ensure_aux(ctx, (hipStream_t)stream, dh::delta_chunk_ws_floats(t) * sizeof(float), &aux);
   if (rc != DH_OK) return rc;
   mark(ctx, kKidConvDelta);
   return hip_status(dh::launch_conv_gated_delta_chunked(p, prev, w, ldp, q, a, b, ldab, a_log, dt_bias, state_in,
-                                                        state_out, o, ctx->aux, t, write_state != 0,
+                                                        state_out, o, aux, t, write_state != 0,
                                                         (hipStream_t)stream),
                     "conv + gated_delta (chunked)");
 }

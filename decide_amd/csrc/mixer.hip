@@ -12,6 +12,7 @@
 
 #include "conv_common.h"
 #include "dh_kernels.h"
+#include "normal_gen.h"
 
 namespace dh {
 
@@ -433,25 +434,12 @@ hipError_t launch_embed_bf16(const uint32_t* ids, const uint16_t* table, float* 
 }
 
 // ---------------------------------------------------------------------------
-// N(mean, σ) fill of fp16 (dtype 0), bf16 (1) or fp32 (2) values from the same
-// counter-based generator as fill_normal_f16: element i depends on (seed, i).
-__device__ __forceinline__ uint64_t mix64b(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  return z ^ (z >> 31);
-}
-
+// N(mean, σ) fill of fp16 (dtype 0), bf16 (1) or fp32 (2) values: element i is
+// normal_at(seed, i, mean, σ) (normal_gen.h) rounded to nearest even.
 __global__ void fill_normal_kernel(void* __restrict__ out, uint64_t n, uint64_t seed, float mean, float sd,
                                    uint32_t dtype) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
-    const uint64_t pidx = i >> 1;
-    const uint64_t a = mix64b(seed + 0x9e3779b97f4a7c15ull * (2 * pidx + 1));
-    const uint64_t b = mix64b(seed + 0x9e3779b97f4a7c15ull * (2 * pidx + 2));
-    const float u1 = ((float)(a >> 40) + 0.5f) * (1.0f / 16777216.0f);
-    const float u2 = ((float)(b >> 40) + 0.5f) * (1.0f / 16777216.0f);
-    const float rad = sqrtf(-2.0f * logf(u1));
-    const float ang = 6.28318530717958647692f * u2;
-    const float zv = ((i & 1) ? rad * sinf(ang) : rad * cosf(ang)) * sd + mean;
+    const float zv = normal_at(seed, i, mean, sd);
     if (dtype == 0) {
       ((_Float16*)out)[i] = (_Float16)zv;
     } else if (dtype == 1) {

@@ -6,6 +6,7 @@
 // final_head), kernels/rmsnorm.metal:8-30 (rmsnorm_rows). All are HBM- or
 // latency-bound; wave64 shuffles for the reductions.
 #include "dh_kernels.h"
+#include "normal_gen.h"
 
 namespace dh {
 
@@ -327,26 +328,12 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, _Float16* y, cons
 }
 
 // ---------------------------------------------------------------------------
-// N(0, σ) fill. Element i takes pair p = i / 2: two uniforms in (0, 1) from
-// the splitmix64 finaliser of (seed, 2p) and (seed, 2p + 1), 24-bit mantissas,
-// then Box–Muller (even i: cos branch, odd i: sin branch), rounded to fp16.
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  return z ^ (z >> 31);
-}
-
+// N(0, σ) fill rounded to fp16: element i is normal_at(seed, i) (normal_gen.h),
+// so it depends only on (seed, i) and a host can reproduce its bits.
 __global__ void fill_normal_f16_kernel(uint16_t* __restrict__ out, uint64_t n, uint64_t seed, float sd) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
-    const uint64_t pidx = i >> 1;
-    const uint64_t a = mix64(seed + 0x9e3779b97f4a7c15ull * (2 * pidx + 1));
-    const uint64_t b = mix64(seed + 0x9e3779b97f4a7c15ull * (2 * pidx + 2));
-    const float u1 = ((float)(a >> 40) + 0.5f) * (1.0f / 16777216.0f);
-    const float u2 = ((float)(b >> 40) + 0.5f) * (1.0f / 16777216.0f);
-    const float rad = sqrtf(-2.0f * logf(u1));
-    const float ang = 6.28318530717958647692f * u2;
-    const float z = (i & 1) ? rad * sinf(ang) : rad * cosf(ang);
-    const _Float16 hv = (_Float16)(z * sd);
+    const float z = normal_at(seed, i, 0.0f, sd);
+    const _Float16 hv = (_Float16)z;
     out[i] = __builtin_bit_cast(uint16_t, hv);
   }
 }

@@ -48,6 +48,12 @@ def rt() -> ctypes.CDLL:
         "hipEventElapsedTime": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
         "hipGetErrorString": (c_char_p, [c_int]),
         "hipGetLastError": (c_int, []),
+        "hipStreamBeginCapture": (c_int, [c_void_p, c_int]),
+        "hipStreamEndCapture": (c_int, [c_void_p, POINTER(c_void_p)]),
+        "hipGraphInstantiate": (c_int, [POINTER(c_void_p), c_void_p, c_void_p, c_void_p, c_size_t]),
+        "hipGraphLaunch": (c_int, [c_void_p, c_void_p]),
+        "hipGraphExecDestroy": (c_int, [c_void_p]),
+        "hipGraphDestroy": (c_int, [c_void_p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(r, name)

@@ -2,17 +2,20 @@
 
 decide's tests draw uniform inputs from ``StdRng`` (testutil.rs:4-8); the
 BASELINE shapes ask for Gaussians instead (X ~ N(0, 1), W ~ N(0, 0.02)), so
-this module defines its own portable generator, the same one the library's
-``dh_fill_normal_f16`` kernel uses on the device:
+this module defines its own portable generator (the library's device fills,
+``dh_fill_normal`` and ``dh_model_init_random``, use the same stream):
 
 * uniform u64 stream: ``mix64(seed + φ·(i + 1))`` with splitmix64's finaliser
   and φ = 0x9e3779b97f4a7c15 (all arithmetic mod 2⁶⁴);
 * pair p of normals from u64s 2p and 2p + 1: 24-bit uniforms in (0, 1),
   Box–Muller, cos branch for even elements and sin branch for odd ones.
 
-The host version computes Box–Muller in float64, the device in float32, so
-the two agree to within fp16 rounding, not bit for bit; tests that compare
-the GPU with the oracle always feed both the same fp16 arrays.
+This host version computes Box–Muller in float64 with numpy's log/cos/sin. The
+device computes it in fp32 from IEEE-rounded +, −, ×, ÷ and sqrt only
+(``decide_amd/csrc/normal_gen.h``), so the two agree to about 1e-6 (1e-4 where
+u₁'s fp32 rounding matters, next to 1), not bit for bit: tests that compare
+the GPU with the oracle feed both the same fp16 arrays, or rebuild device
+fills with the oracle's bit-exact restatement of the device steps.
 """
 
 from __future__ import annotations

@@ -13,15 +13,31 @@
  *     calling thread's dh_last_error() holds a one-line message. Contract
  *     violations are reported before anything is launched.
  * The library never allocates or frees caller memory. A context owns only its
- * launch plan and two workspaces (device memory it allocates itself): the
- * split-K partials and the forward kernels' scratch. A context is immutable
- * after dh_ctx_create apart from those workspaces, which grow under an
- * internal lock; launches on different streams that share a context must not
- * run split-K GEMMs concurrently (they share the workspace). A workspace that
- * grows is replaced, and the buffer it replaces stays allocated until
- * dh_ctx_destroy, so a graph captured earlier (dh_model_capture) never reads
- * freed memory; it keeps reading the buffers it was captured with, so replays
- * of one graph must not overlap work that uses those buffers.
+ * launch plan and, per stream that uses it, two workspaces (device memory it
+ * allocates itself): the split-K partials and the forward kernels' scratch
+ * (attention's key pieces and the chunked recurrence's per-chunk matrices).
+ * Threads and streams (decide: Gemm is Sync, its pipeline cache behind a
+ * mutex, kernels/gemm.rs:46-55, 115-124):
+ *   - a context may be shared by host threads and by streams. Its plan is
+ *     fixed after dh_ctx_create (dh_gemm_force aside, which is atomic and
+ *     meant for tuning), and each stream gets its own workspaces, allocated on
+ *     that stream's first call that needs them and grown under an internal
+ *     lock, so calls on different streams may overlap;
+ *   - a workspace that grows is replaced, and the buffer it replaces stays
+ *     allocated until dh_ctx_destroy, so a graph captured earlier
+ *     (dh_model_capture) never reads freed memory; a graph keeps using the
+ *     workspaces of the stream it was captured on, so its replays must not
+ *     overlap other calls on that stream's workspaces;
+ *   - a workspace never grows while its stream is being captured: such a call
+ *     returns DH_EINVAL (size it first with dh_warm_up or an eager call of the
+ *     same size on that stream);
+ *   - a stream's workspaces stay with the context until dh_ctx_destroy, and a
+ *     stream created later with the same handle reuses them: destroy a stream
+ *     only after its work has finished;
+ *   - dh_gemm_nt_noalloc's scratch is one array per GPU, shared by every
+ *     context on it: its calls must not overlap on one GPU;
+ *   - a dh_model (its activations, caches and request state) serves one
+ *     request at a time: calls on one model must not overlap.
  */
 #ifndef DECIDE_HIP_H
 #define DECIDE_HIP_H
@@ -84,7 +100,11 @@ typedef struct dh_gemm_plan {
 } dh_gemm_plan;
 
 /* --- context (decide: Gemm::new / Gemm::with_impl, kernels/gemm.rs:56-83;
- *     Kernels::new, kernels/mod.rs:53-67) --- */
+ *     Kernels::new, kernels/mod.rs:53-67) ---
+ * Creates a context on the current device (which must be gfx950). Its first
+ * creation on a device also takes that device's no-allocation scratch
+ * (DH_NOALLOC_SCRATCH_BYTES, shared by every context on the device until the
+ * process ends; see dh_gemm_nt_noalloc). Workspaces are per stream (above). */
 int dh_ctx_create(uint32_t flags, dh_ctx** out);
 void dh_ctx_destroy(dh_ctx* ctx);
 /* The calling thread's message for its last failed call ("" if none). */
@@ -93,8 +113,14 @@ const char* dh_last_error(void);
 const char* dh_version(void);
 
 /* Loads every kernel of the menu and runs each once on a tiny shape, and sizes
- * the split-K workspace for `max_m` rows of the widest planned GEMM, so a timed
- * forward neither loads code nor allocates (decide: Gemm::warm_up, gemm.rs:87-107). */
+ * `stream`'s workspaces so that a timed forward of up to `max_m` rows on that
+ * stream neither loads code nor allocates (decide: Gemm::warm_up,
+ * gemm.rs:87-107): the split-K workspace for the largest split plan of decide's
+ * engine shapes at any M up to max_m, and the forward kernels' workspace, whose
+ * attention part is sized even for a GEMM-only context: 8.4 MB at max_m = 1,
+ * growing with max_m to 84.5 MB (plus the chunked recurrence's, from
+ * DH_DELTA_CHUNK_MIN_T rows). max_m must be in 1..DH_PLAN_MAX_ROWS. */
+#define DH_PLAN_MAX_ROWS 65536u
 int dh_warm_up(dh_ctx* ctx, void* stream, uint32_t max_m);
 /* Distinct kernels launched through this context so far; after dh_warm_up it
  * must not grow (decide: Gemm::fast_pipelines, gemm.rs:109-113; engine.rs:163-172). */
@@ -143,11 +169,15 @@ int dh_gemm_nt_grouped(dh_ctx* ctx, void* stream, const void* x, uint32_t ldx, u
 int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint32_t epi, dh_gemm_plan* out);
 /* The split-K workspace (bytes) that dh_gemm_nt's planner asks for at its
  * largest over every m in 1..max_m and every epilogue at (n, k), on this
- * context (no device needed). dh_warm_up holds at least this for decide's
- * engine shapes; a caller with other shapes can size its own calls with it. */
+ * context (no device needed; the planner runs once per m, so max_m is capped
+ * at DH_PLAN_MAX_ROWS, about 0.3 s of host time per shape there). dh_warm_up
+ * holds at least this for decide's engine shapes; a caller with other shapes
+ * can size its own calls with it. */
 int dh_gemm_ws_need(const dh_ctx* ctx, uint32_t max_m, uint32_t n, uint32_t k, uint64_t* out);
-/* Forces the next GEMMs on this context to use `variant` and `splits`
- * (variant = UINT32_MAX restores the planner). For tuning sweeps only. */
+/* Forces the next GEMMs on this context, on every stream, to use `variant` and
+ * `splits` (variant = UINT32_MAX restores the planner). For tuning sweeps
+ * only: calls already running in other threads see the change at their next
+ * plan. */
 int dh_gemm_force(dh_ctx* ctx, uint32_t variant, uint32_t splits);
 /* Number of compiled tile variants and the geometry of one of them: the tile's
  * rows and columns, its wavefronts (4, or 8 with two per SIMD) and the columns

@@ -22,6 +22,12 @@
  *   orc_interleave_gate_up / orc_deinterleave_q_gate
  *                        hand-written permutation KATs.
  *   orc_gemm_f32_fast    agrees with orc_gemm_nt within fp32 rounding.
+ *   orc_fill_normal      the library's own seeded Gaussian (not a decide
+ *                        function: it makes the random-init weights), restated
+ *                        so the host can rebuild a random-init model bit for bit;
+ *                        checked bitwise against a numpy float32 restatement,
+ *                        against float64 Box–Muller (math.log/cos/sin) within
+ *                        fp32 rounding, and by its moments.
  * Build: oracle/Makefile (gcc -O2 -fopenmp, no -ffast-math: sums stay in order).
  */
 #include <math.h>
@@ -297,4 +303,94 @@ int64_t orc_assert_close(const float* got, const float* want, size_t n, float at
     }
   }
   return worst;
+}
+
+/* ---------- seeded Gaussian: the library's random-init generator, restated ----------
+ * Element i of the stream with seed s (decide_amd/csrc/normal_gen.h states the
+ * same steps for the device): two 24-bit uniforms a, b from splitmix64's
+ * finaliser over s + φ(2p+1) and s + φ(2p+2), p = i/2; Box–Muller with
+ * r = sqrt(−2 ln u1), u1 = (a + ½)·2⁻²⁴, and θ = 2π(b + ½)·2⁻²⁴ = (π/4)(o + t)
+ * (octant o = b's top 3 bits, t from the other 21); even i: r·cos θ, odd i:
+ * r·sin θ; value = (r·trig)·sd + mean, then RNE to the tensor's type.
+ * Only IEEE-rounded fp32 +, −, ×, ÷ and sqrt, in this order, no contraction
+ * (-ffp-contract=off): ln via the atanh series on m ∈ [√½, √2), sin/cos of
+ * (π/4)t via Taylor series; constants are the fp32 roundings of 1/k, ln 2,
+ * √2 and ±(π/4)^k/k!. */
+static uint64_t nrm_mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+static float nrm_ln(float u) {
+  const uint32_t bits = f2u(u);
+  int e = (int)(bits >> 23) - 127;
+  float m = u2f((bits & 0x7fffffu) | 0x3f800000u);
+  if (m > 0x1.6a09e6p+0f) {
+    m = m * 0.5f;
+    e = e + 1;
+  }
+  const float z = (m - 1.0f) / (m + 1.0f);
+  const float z2 = z * z;
+  float p = 0x1.745d18p-4f;
+  p = p * z2 + 0x1.c71c72p-4f;
+  p = p * z2 + 0x1.24924ap-3f;
+  p = p * z2 + 0x1.99999ap-3f;
+  p = p * z2 + 0x1.555556p-2f;
+  p = p * z2 + 1.0f;
+  return (float)e * 0x1.62e430p-1f + (z + z) * p;
+}
+
+static void nrm_sincos(float t, float* s, float* c) {
+  const float t2 = t * t;
+  float ps = -0x1.e30750p-30f;
+  ps = ps * t2 + 0x1.507834p-22f;
+  ps = ps * t2 - 0x1.32d2ccp-15f;
+  ps = ps * t2 + 0x1.466bc6p-9f;
+  ps = ps * t2 - 0x1.4abbcep-4f;
+  ps = ps * t2 + 0x1.921fb6p-1f;
+  *s = t * ps;
+  float pc = 0x1.f9d38ap-34f;
+  pc = pc * t2 - 0x1.a6d1f2p-26f;
+  pc = pc * t2 + 0x1.e1f506p-19f;
+  pc = pc * t2 - 0x1.55d3c8p-12f;
+  pc = pc * t2 + 0x1.03c1f0p-6f;
+  pc = pc * t2 - 0x1.3bd3ccp-2f;
+  *c = pc * t2 + 1.0f;
+}
+
+float orc_normal_at(uint64_t seed, uint64_t i, float mean, float sd) {
+  const uint64_t p = i >> 1, phi = 0x9e3779b97f4a7c15ull;
+  const uint32_t a = (uint32_t)(nrm_mix64(seed + phi * (2 * p + 1)) >> 40);
+  const uint32_t b = (uint32_t)(nrm_mix64(seed + phi * (2 * p + 2)) >> 40);
+  const float r = sqrtf(-2.0f * nrm_ln(((float)a + 0.5f) * 0x1p-24f));
+  const uint32_t o = b >> 21;
+  const float t = ((float)(b & 0x1fffffu) + 0.5f) * 0x1p-21f;
+  float sb, cb;
+  nrm_sincos((o & 1u) ? 1.0f - t : t, &sb, &cb);
+  if (o & 1u) sb = -sb;
+  /* θ = k·π/2 + β, β = ±(π/4)·(t or 1 − t): rotate (cos β, sin β) by k quarter turns */
+  const uint32_t k = ((o + 1u) >> 1) & 3u;
+  const float cth = k == 0 ? cb : k == 1 ? -sb : k == 2 ? -cb : sb;
+  const float sth = k == 0 ? sb : k == 1 ? cb : k == 2 ? -sb : -cb;
+  const float z = r * ((i & 1) ? sth : cth);
+  return z * sd + mean;
+}
+
+/* n values of the stream into out as fp16 (dtype 0), bf16 (1) or fp32 (2) bits. */
+void orc_fill_normal(void* out, uint64_t n, uint64_t seed, float mean, float sd, uint32_t dtype, int threads) {
+#ifdef _OPENMP
+  if (threads < 1) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static, 65536)
+#endif
+  for (int64_t ii = 0; ii < (int64_t)n; ++ii) {
+    const uint64_t i = (uint64_t)ii;
+    const float v = orc_normal_at(seed, i, mean, sd);
+    if (dtype == 0)
+      ((uint16_t*)out)[i] = orc_f16_from_f32(v);
+    else if (dtype == 1)
+      ((uint16_t*)out)[i] = orc_bf16_from_f32(v);
+    else
+      ((float*)out)[i] = v;
+  }
 }

@@ -13,6 +13,7 @@ import numpy as np
 import oracle_lib as orc
 
 HIDDEN = 2560
+INTER = 9216
 LIN_Z, LIN_B, LIN_A = 8192, 12288, 12320
 Q_DIM, KV_DIM, ATT_K, ATT_V = 4096, 1024, 8192, 9216
 NV, DV, DK = 32, 128, 128
@@ -87,3 +88,58 @@ def forward(W: dict, layers: int, ids: np.ndarray, ans_rows: np.ndarray, cand: n
     if xs is None:
         xs = x[ans_rows]
     return orc.final_head(xs, W["final_norm"], W["embed"], cand, ncand, max_cand)
+
+
+# ---- random-init models rebuilt on the host ----------------------------------------------------------------------
+# dh_model_init_random(seed) fills tensor i of the model's registry with the stream
+# seed + φ·(i + 1) (mod 2^64) of the library's seeded Gaussian, which orc_fill_normal restates bit for bit.
+PHI = 0x9E3779B97F4A7C15
+F16, BF16, F32 = 0, 1, 2
+
+
+def random_init_registry(layers: int, vocab: int) -> list[tuple[str, tuple, int, float, float]]:
+    """(name, shape, dtype code, mean, std) in dh_model_create's registration order: embed, final_norm, then per
+    layer in_norm, the mixer's tensors (attention: w_in, q_norm, k_norm, w_out; Gated-DeltaNet: w_in, conv_w, a_log,
+    dt_bias, gnorm, w_out), post_norm, w_gu, w_down. Shapes are the [N, K] GEMM layouts."""
+    reg = [("embed", (vocab, HIDDEN), BF16, 0.0, 0.02), ("final_norm", (HIDDEN,), F32, 0.0, 0.02)]
+    for l in range(layers):
+        pre = f"L{l}."
+        reg.append((pre + "in_norm", (HIDDEN,), F32, 0.0, 0.02))
+        if (l + 1) % 4 == 0:
+            reg += [(pre + "w_in", (ATT_V + KV_DIM, HIDDEN), F16, 0.0, 0.02), (pre + "q_norm", (256,), F32, 0.0, 0.02),
+                    (pre + "k_norm", (256,), F32, 0.0, 0.02), (pre + "w_out", (HIDDEN, Q_DIM), F16, 0.0, 0.02)]
+        else:
+            reg += [(pre + "w_in", (LIN_A + NV, HIDDEN), F16, 0.0, 0.02),
+                    (pre + "conv_w", (orc.CONV_DIM, 4), F32, 0.0, 0.3), (pre + "a_log", (NV,), F32, 0.5, 0.5),
+                    (pre + "dt_bias", (NV,), F32, 0.0, 0.5), (pre + "gnorm", (DV,), F32, 1.0, 0.02),
+                    (pre + "w_out", (HIDDEN, NV * DV), F16, 0.0, 0.02)]
+        reg += [(pre + "post_norm", (HIDDEN,), F32, 0.0, 0.02), (pre + "w_gu", (2 * INTER, HIDDEN), F16, 0.0, 0.02),
+                (pre + "w_down", (HIDDEN, INTER), F16, 0.0, 0.02)]
+    return reg
+
+
+def random_init_tensor(seed: int, index: int, shape, dtype: int, mean: float, std: float) -> np.ndarray:
+    """Tensor `index` of a model after dh_model_init_random(seed), as forward() takes it (bf16 as raw bits)."""
+    n = int(np.prod(shape))
+    return orc.fill_normal(n, (seed + PHI * (index + 1)) % 2**64, mean, std, dtype).reshape(shape)
+
+
+class RandomInitWeights:
+    """The weights of dh_model_init_random(seed) for a (layers, vocab) model, generated on first use. Keeps the
+    embedding and the most recent `keep` other tensors, so a deep forward needs about one layer's weights at once."""
+
+    def __init__(self, seed: int, layers: int, vocab: int, keep: int = 12):
+        self.seed = seed
+        self.reg = {name: (i, shape, dt, mean, std)
+                    for i, (name, shape, dt, mean, std) in enumerate(random_init_registry(layers, vocab))}
+        self.keep = keep
+        self.cache: dict[str, np.ndarray] = {}
+
+    def __getitem__(self, name: str) -> np.ndarray:
+        if name not in self.cache:
+            i, shape, dt, mean, std = self.reg[name]
+            others = [k for k in self.cache if k != "embed"]
+            if len(others) >= self.keep:
+                del self.cache[others[0]]
+            self.cache[name] = random_init_tensor(self.seed, i, shape, dt, mean, std)
+        return self.cache[name]

@@ -65,6 +65,8 @@ def load() -> ctypes.CDLL:
         "orc_head_norm_rope": (None, [c_void_p, c_void_p, c_uint32, c_void_p]),
         "orc_attention": (None, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
         "orc_embed_bf16": (None, [c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
+        "orc_normal_at": (c_float, [ctypes.c_uint64, ctypes.c_uint64, c_float, c_float]),
+        "orc_fill_normal": (None, [c_void_p, ctypes.c_uint64, ctypes.c_uint64, c_float, c_float, c_uint32, c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -269,4 +271,12 @@ def embed_bf16(ids, table_bits) -> np.ndarray:
     table_bits = np.ascontiguousarray(table_bits, dtype=np.uint16)
     out = np.empty((len(ids), table_bits.shape[1]), np.float32)
     load().orc_embed_bf16(_p(ids), _p(table_bits), len(ids), table_bits.shape[1], _p(out))
+    return out
+
+
+def fill_normal(n: int, seed: int, mean: float, sd: float, dtype: int, threads: int = 0) -> np.ndarray:
+    """The library's random-init stream restated (orc_fill_normal): n values ~ N(mean, sd) as fp16 (dtype 0),
+    bf16 bits as uint16 (1) or fp32 (2); element i depends only on (seed, i)."""
+    out = np.empty(n, dtype={0: np.float16, 1: np.uint16, 2: np.float32}[dtype])
+    load().orc_fill_normal(_p(out), n, seed & (2**64 - 1), mean, sd, dtype, threads)
     return out

@@ -276,3 +276,15 @@ def test_workspace_need_covers_every_m(kn):
     # the point of the sweep: a larger M can need less than a smaller one
     if kn == (9216, 2560):
         assert plan_for(1146, n, k, Epilogue.AddF32)["ws_bytes"] > plan_for(2307, n, k, Epilogue.AddF32)["ws_bytes"]
+
+
+def test_workspace_need_refuses_an_unbounded_sweep():
+    """dh_gemm_ws_need runs the planner once per M, so max_m is capped (DH_PLAN_MAX_ROWS = 65,536): beyond it the
+    call is refused at once instead of spending hours of host time."""
+    lib = _lib.load()
+    need = ctypes.c_uint64(7)
+    assert lib.dh_gemm_ws_need(None, 0xFFFFFFFF, 2560, 9216, ctypes.byref(need)) == _lib.DH_EINVAL
+    assert "DH_PLAN_MAX_ROWS" in _lib.last_error()
+    assert lib.dh_gemm_ws_need(None, 65537, 2560, 9216, ctypes.byref(need)) == _lib.DH_EINVAL
+    assert need.value == 7  # untouched
+    assert lib.dh_warm_up(None, None, 65537) == _lib.DH_EINVAL  # null context is reported first, without a device

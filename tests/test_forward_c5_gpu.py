@@ -1,22 +1,26 @@
 """BASELINE config 5 at the size its targets are stated on: the 4B-shaped hybrid forward (36 layers, every 4th
 full attention, d 2560, d_ff 9216) over a 2,307-token prompt, bar max |Δlogit| <= 0.01.
 
-The oracle forward (tests/oracle_forward.py: cpu_ref.rs pieces with decide's rounding points, forward.rs:1118-1310)
-runs at the extremes the CPU can finish in well under a minute each:
+The stated shape itself (36 layers, T = 2,307, vocab 151,936, 3 answers x 8 candidates, one list ragged) against
+the oracle: the random-init model is rebuilt bit for bit on the host (the device fill's steps restated in
+orc_fill_normal) and tests/golden/c5_full_logits.npz holds the oracle forward's logits for it (tests/oracle_forward.py:
+cpu_ref.rs pieces with decide's rounding points, forward.rs:1118-1310), with f64 GEMM sums and, as the fp32 noise
+floor at this shape, with fp32 sums (tests/golden/make_forward_logits.py c5). Measured: GPU 0.0084, fp32-sum oracle
+0.0093.
+The live oracle also runs at the extremes the CPU finishes in well under a minute each:
   * length: 4 layers at T = 2,307 (the chunked recurrence over 2,307 steps and 2,307-key causal attention over every
-    row, no pruning), bar 0.01;
-  * depth: 24 layers at T = 256, bar 0.01, and all 36 layers at T = 256 (the last one pruned to 3 answer rows);
-  * 8 layers at T = 603, the shorter prompt length BASELINE reports, bar 0.01.
-At 36 layers this random-init model amplifies fp32-level differences to about the size of the bar itself: the same
-oracle with its GEMM sums in fp32 (orc_gemm_f32_fast) instead of f64 differs from the f64 oracle by 0.006-0.013 in
-max |Δlogit| over six seed/init choices, and the GPU forward by 0.007-0.011. So the 36-layer test computes that
-fp32 noise floor beside the GPU's difference, reports both, and holds the GPU to 0.015.
-The full shape itself (36 layers, T = 2,307, vocab 151,936, 3 answers x 8 candidates) is checked through properties
-that need no oracle: bitwise run-to-run determinism, graph replay equal to eager, pruned within 1e-3 of unpruned,
-agreement with an independent GPU implementation (the M-independent reference GEMM kernel and the token-by-token
-recurrence) within 0.025 (at this length a one-ulp change in a fraction of the fp16 activations alone moves the
-logits by up to 0.009; see IMPL_NOISE_BOUND), and one closed form of the layer wiring: with every w_out and w_down zero the
-residual stream never leaves the embedding rows, so the logits are final_head of the answers' embedding rows."""
+    row, no pruning);
+  * depth: 24 and 36 layers at T = 256 (the last one pruned to 3 answer rows), the latter beside the fp32-sum oracle;
+  * 8 layers at T = 603, the shorter prompt length BASELINE reports;
+all at the bar 0.01.
+The full shape is further checked through properties that need no oracle: bitwise run-to-run determinism, graph
+replay equal to eager, pruned within 1e-3 of unpruned, agreement with an independent GPU implementation (the
+M-independent reference GEMM kernel and the token-by-token recurrence) within 0.025 (at this length a one-ulp change
+in a fraction of the fp16 activations alone moves the logits by up to 0.009; see IMPL_NOISE_BOUND), and one closed
+form of the layer wiring: with every w_out and w_down zero the residual stream never leaves the embedding rows, so
+the logits are final_head of the answers' embedding rows."""
+
+import os
 
 import numpy as np
 import pytest
@@ -33,12 +37,11 @@ from test_forward_gpu import MAX_LOGIT_DIFF, _names, _shape
 pytestmark = pytest.mark.gpu
 
 LAYERS, T_FULL, VOCAB, ANSWERS, CANDS = 36, 2307, 151936, 3, 8
-# At 36 layers two correct fp32 implementations differ by about the bar itself (see the module docstring).
-FP32_NOISE_BOUND = 0.015
-# The full shape (36 layers over 2,307 tokens) amplifies ulp-level differences further. Measured on MI355X with
-# this build's kernels: rounding about 1 in 10^4 SwiGLU outputs once instead of twice (fp16 directly, against
-# fp32 then fp16; one fp16 ulp apart) moves these logits by 0.006-0.009, and the fast path and the reference
-# implementations differ by 0.006, 0.010 and 0.018 for three random inits (0.009-0.012 with the single rounding).
+# Two fp32 implementations on the GPU differ by more than either differs from the f64 oracle, since each sits on its
+# own side of it. At the stated shape the fast path is 0.0084 from the oracle and the fp32-sum oracle 0.0093
+# (test_full_shape_matches_the_oracle); the fast path and the reference implementations (M-independent GEMM kernel,
+# token-by-token recurrence) measure 0.0153 apart in this test. The bar below was set before the stated-shape oracle
+# existed; the oracle comparison above is the parity test of record.
 IMPL_NOISE_BOUND = 0.025
 
 
@@ -119,7 +122,7 @@ def test_forward_at_full_depth_is_within_the_fp32_noise_floor(gpu, kernels):
     """All 36 layers at T = 256 against the f64 oracle, beside the same oracle with fp32 GEMM sums."""
     diff, floor = _oracle_drift(kernels, LAYERS, 256, True, seed=5100, noise_floor=True)
     assert floor > 0.0
-    assert diff <= FP32_NOISE_BOUND, f"max |Δlogit| {diff:.4g} (fp32-sum oracle: {floor:.4g})"
+    assert diff <= MAX_LOGIT_DIFF, f"max |Δlogit| {diff:.4g} (fp32-sum oracle: {floor:.4g})"
 
 
 @pytest.fixture(scope="module")
@@ -136,6 +139,26 @@ def full_model(kernels):
 @pytest.fixture(scope="module")
 def full_request():
     return _request(T_FULL, VOCAB, 5300)
+
+
+def test_full_shape_matches_the_oracle(gpu, full_model, full_request):
+    """The stated shape itself against the oracle: tests/golden/c5_full_logits.npz holds the oracle forward's logits
+    for this model (dh_model_init_random(0xDEC1DE), rebuilt bit for bit on the host) and this request, with f64 GEMM
+    sums and, as the fp32 noise floor at this shape, with fp32 sums (tests/golden/make_forward_logits.py c5)."""
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "c5_full_logits.npz"))
+    layers, t, vocab, answers, cands, init_seed = (int(v) for v in fx["meta"][:6])
+    assert (layers, t, vocab, answers, cands, init_seed) == (LAYERS, T_FULL, VOCAB, ANSWERS, CANDS, 0xDEC1DE)
+    for name, a in zip(("ids", "ans", "cand", "ncand"), full_request):
+        np.testing.assert_array_equal(a, fx[name], err_msg=name)
+    got = _forward(full_model, *full_request)
+    want, alt = fx["logits_f64"], fx["logits_f32sum"]
+    written = ~np.isnan(want)
+    assert np.array_equal(~np.isnan(got), written)
+    diff = float(np.abs(got[written] - want[written]).max())
+    floor = float(np.abs(alt[written] - want[written]).max())
+    print(f"36 layers, T 2307: GPU max |Δlogit| {diff:.4f}, fp32-sum oracle {floor:.4f} "
+          f"(logits up to {np.abs(want[written]).max():.3g})")
+    assert diff <= MAX_LOGIT_DIFF, f"max |Δlogit| {diff:.4g} (fp32-sum oracle: {floor:.4g})"
 
 
 def test_full_shape_is_finite_and_deterministic(gpu, full_model, full_request):
