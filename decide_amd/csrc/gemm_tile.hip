@@ -236,12 +236,129 @@ __device__ __forceinline__ void store_tile_lds(f4 (&acc)[FM][FN], const TileArgs
   });
 }
 
+// Epilogue of the 2 x 2 tiles with swapped MFMA operands (Pipe<..., SW>): lane (r, g) of a wave holds, for
+// fragment (i, j), row 16i + r and columns 16j + 4g .. +3 of the wave's block, so every output leaves straight
+// from registers: fp32 / fp16 / split-K partials as 16- or 8-byte stores of 4 consecutive columns, SwiGLU as
+// 8-byte stores of 4 outputs from a whole gate|up pair. Only the pair that straddles the two N halves (FN odd:
+// the left waves hold its gate, the right waves its up) passes through LDS, in fp32. The values stored are
+// those of store_tile_lds, bit for bit.
+template <int FM, int FN>
+__device__ __forceinline__ void store_tile_sw(f4 (&acc)[FM][FN], const TileArgs& p, int mi, uint32_t split,
+                                              uint32_t m0, uint32_t n0, int wave, int r, int g, float* stage) {
+  static_assert(FN % 2 == 1, "2 x 2 layouts: SwiGLU handles one straddling pair (odd fragments per wave)");
+  constexpr int WN = 2;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  typedef float fl2 __attribute__((ext_vector_type(2)));
+  const int wm = wave / WN, wn = wave % WN, lane = r + 16 * g;
+  const uint32_t rbase = (uint32_t)(wm * 16 * FM), cbase = (uint32_t)(wn * 16 * FN);
+  const uint32_t M = p.m, N = p.mem[mi].n;
+  const uint32_t epi = p.mem[mi].epi, ldy = p.mem[mi].ldy;
+  char* Y = (char*)p.mem[mi].y;
+  const bool partial = p.splits > 1;
+  if (epi == 3u && !partial) {
+    const bool v8 = (((uintptr_t)Y) % 8) == 0 && ((size_t)ldy * 2) % 8 == 0;
+    // four outputs silu(g)·u of one row at output column ocol (a multiple of 4)
+    auto put = [&](uint32_t grow, uint32_t ocol, const f4& gv, const f4& uv) {
+      h4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (_Float16)swiglu_f(gv[e], uv[e]);
+      _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + ocol;
+      if (v8) {
+        *(h4*)dst = o;  // a quarter line per 16 lanes: plain stores, so L2 merges the lines before HBM
+      } else {
+        *(h2*)dst = h2{o[0], o[1]};
+        *(h2*)(dst + 2) = h2{o[2], o[3]};
+      }
+    };
+    f4* xch = (f4*)stage + wm * FM * 64;  // the straddling pair's gate, [FM][64 lanes] per M half
+    __syncthreads();                      // every wave is past its last read of the main loop's LDS
+    if (wn == 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        pin_acc(acc[i][FN - 1]);
+        xch[i * 64 + lane] = acc[i][FN - 1];
+      }
+    }
+    auto pairs = [&](auto wnc) {
+      constexpr int J0 = decltype(wnc)::value;  // the first local fragment that starts a whole pair
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const uint32_t grow = m0 + rbase + 16 * i + r;
+        static_for<0, (FN - J0) / 2>([&](auto qc) {
+          constexpr int j = J0 + 2 * decltype(qc)::value;
+          pin_acc(acc[i][j]);
+          pin_acc(acc[i][j + 1]);
+          const uint32_t gcol = n0 + cbase + 16 * j;  // the pair's gate block, a multiple of 32
+          if (grow < M && gcol < N) put(grow, gcol / 2 + 4 * g, acc[i][j], acc[i][j + 1]);
+        });
+      }
+    };
+    if (wn == 0)
+      pairs(std::integral_constant<int, 0>{});
+    else
+      pairs(std::integral_constant<int, 1>{});
+    __syncthreads();
+    if (wn == 1) {
+      const uint32_t gcol = n0 + 16 * (FN - 1);  // the straddling pair's gate block
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const uint32_t grow = m0 + rbase + 16 * i + r;
+        pin_acc(acc[i][0]);
+        const f4 gv = xch[i * 64 + lane];
+        if (grow < M && gcol < N) put(grow, gcol / 2 + 4 * g, gv, acc[i][0]);
+      }
+    }
+    return;
+  }
+  const uint32_t esz = (partial || epi == 0u || epi == 2u) ? 4u : 2u;
+  const bool vec = partial || ((((uintptr_t)Y) % (4 * esz)) == 0 && ((size_t)ldy * esz) % (4 * esz) == 0);
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const uint32_t grow = m0 + rbase + 16 * i + r;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      pin_acc(acc[i][j]);
+      const uint32_t gcol = n0 + cbase + 16 * j + 4 * g;
+      if (grow >= M || gcol >= N) continue;
+      const f4 v = acc[i][j];
+      if (partial) {
+        *(f4*)(p.ws + ((size_t)split * M + grow) * N + gcol) = v;
+      } else if (epi == 1u) {
+        _Float16* dst = (_Float16*)Y + (size_t)grow * ldy + gcol;
+        const h4 o = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+        if (vec) {
+          *(h4*)dst = o;
+        } else {
+          *(h2*)dst = h2{o[0], o[1]};
+          *(h2*)(dst + 2) = h2{o[2], o[3]};
+        }
+      } else {
+        float* dst = (float*)Y + (size_t)grow * ldy + gcol;
+        if (vec) {
+          f4 o = v;
+          if (epi == 2u) o += *(const f4*)dst;
+          *(f4*)dst = o;
+        } else {
+          fl2 lo = fl2{v[0], v[1]}, hi = fl2{v[2], v[3]};
+          if (epi == 2u) {
+            lo += *(const fl2*)dst;
+            hi += *(const fl2*)(dst + 2);
+          }
+          *(fl2*)dst = lo;
+          *(fl2*)(dst + 2) = hi;
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // The tile pipeline: NBX X-tile and NBW W-tile stage buffers; stage kt issues
 // X(kt + NBX - 1) and W(kt + NBW - 1). The DMAs a stage issues are ordered so
 // that the ones needed by the next stage come first; one vmcnt wait then
 // covers exactly those.
-template <int FM, int FN_, int WM, int NBX, int NBW>
+template <int FM, int FN_, int WM, int NBX, int NBW, bool SW = false>
 struct Pipe {
   static constexpr int FN = FN_, WN = 4 / WM, NT = 256, LAX = NBX - 1, LAW = NBW - 1;
   static constexpr int U = (NBX == NBW) ? NBX : NBX * NBW;  // unroll (lcm for 2, 3)
@@ -263,6 +380,15 @@ struct Pipe {
   static_assert(BN % 32 == 0, "whole 8-row DMA groups per wave");
 
   f4 acc[FM][FN];
+  // acc += X fragment · W fragmentᵀ. With SW the MFMA takes W as its A operand, so each accumulator holds its
+  // 16 x 16 block transposed (lane (r, g): row r, columns 4g .. 4g+3); swapping the operands leaves every sum
+  // bitwise the same.
+  __device__ __forceinline__ static void mma(f4& c, const h8& xa, const h8& wb) {
+    if constexpr (SW)
+      mfma_acc_v(c, wb, xa);
+    else
+      mfma_acc_v(c, xa, wb);
+  }
   uint32_t xoff[XPW];
   uint32_t woff[WPW];
   uint32_t a0, a1;
@@ -363,7 +489,7 @@ struct Pipe {
         }
       }
 #pragma unroll
-      for (int j = 0; j < FN; ++j) mfma_acc_v(acc[f % FM][j], a[f % (AD + 1)], wf[j][f / FM]);
+      for (int j = 0; j < FN; ++j) mma(acc[f % FM][j], a[f % (AD + 1)], wf[j][f / FM]);
     });
   }
   // Stage kt; U-periodic slot indices are compile-time via Q = kt mod U.
@@ -500,18 +626,18 @@ struct Pipe {
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         if constexpr (RA)
-          mfma_acc_v(acc[r][s], rf[h][r], sf[h][s]);
+          mma(acc[r][s], rf[h][r], sf[h][s]);
         else
-          mfma_acc_v(acc[s][r], sf[h][s], rf[h][r]);
+          mma(acc[s][r], sf[h][s], rf[h][r]);
       }
     });
   }
 };
 
 // One tile: FM x FN fragments per wave, WM waves along M and 4 / WM along N.
-template <int FM, int FN, int WM, int NBX, int NBW>
+template <int FM, int FN, int WM, int NBX, int NBW, bool SW = false>
 __device__ __forceinline__ void tile_body(const TileArgs& p) {
-  using P = Pipe<FM, FN, WM, NBX, NBW>;
+  using P = Pipe<FM, FN, WM, NBX, NBW, SW>;
   constexpr int BN = P::BN;
   constexpr int LDSB = P::LDS_BYTES > 64 * (BN + 4) * 4 ? P::LDS_BYTES : 64 * (BN + 4) * 4;
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
@@ -666,11 +792,14 @@ __device__ __forceinline__ void tile_body(const TileArgs& p) {
         for (int j = 0; j < FN; ++j) tie(wf[j]);
       }
 #pragma unroll
-      for (int j = 0; j < FN; ++j) mfma_acc_v(pp.acc[i][j], a, wf[j]);
+      for (int j = 0; j < FN; ++j) P::mma(pp.acc[i][j], a, wf[j]);
     });
   }
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  store_tile_lds<FM, FN, WM>(pp.acc, p, mi, split, m0, n0, wave, r, g, (float*)lds);
+  if constexpr (SW)
+    store_tile_sw<FM, FN>(pp.acc, p, mi, split, m0, n0, wave, r, g, (float*)lds);
+  else
+    store_tile_lds<FM, FN, WM>(pp.acc, p, mi, split, m0, n0, wave, r, g, (float*)lds);
 }
 
 template <int FM, int NBX, int NBW>
@@ -681,10 +810,10 @@ void gemm_tile_kernel(const TileArgs p) {
 
 // 2 x 2 waves, each FM x FN fragments: BM = 32·FM, BN = 32·FN. A gate|up
 // pair may straddle the two N halves, so SwiGLU runs from the staged tile.
-template <int FM, int FN, int NBX, int NBW>
+template <int FM, int FN, int NBX, int NBW, bool SW = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_tile22_kernel(const TileArgs p) {
-  tile_body<FM, FN, 2, NBX, NBW>(p);
+  tile_body<FM, FN, 2, NBX, NBW, SW>(p);
 }
 // ---------------------------------------------------------------------------
 // 8-wave BM x BN tiles, two waves per SIMD (BM = 32·FM, BN = 32·(FNA + FNB)). A wave
@@ -1125,15 +1254,16 @@ struct VariantEntry {
 #define DH_TILE_ENTRY(FM, NBX, NBW) {{FM, 4, 4, 1}, gemm_tile_kernel<FM, NBX, NBW>},
 static const VariantEntry kVariants[] = {
     DH_TILE_MENU(DH_TILE_ENTRY)
-    // 96 x 160 with a 5-deep ring: small M (48-96 rows) over wide N
-    {{3, 5, 2, 2}, gemm_tile22_kernel<3, 5, 5, 5>},
+    // 96 x 160 with a 5-deep ring: small M (48-96 rows) over wide N; swapped operands, epilogue from registers
+    {{3, 5, 2, 2}, gemm_tile22_kernel<3, 5, 5, 5, true>},
     // 160 x 288: at M ≈ 603 the gate|up projection is 4 x 64 = 256 tiles, one per CU
     {{5, 9, 2, 2}, gemm_tile22_kernel<5, 9, 2, 3>},
     // 288 x 224 and 224 x 224: the M = 2307 projections in fewer rounds of 256 tiles
     {{9, 7, 2, 2}, gemm_tile22_kernel<9, 7, 2, 3>},
     {{7, 7, 2, 2}, gemm_tile22_kernel<7, 7, 2, 3>},
-    // 160 x 160: the N = 2560 projections (10 % less LDS traffic per output than 96 x 256)
-    {{5, 5, 2, 2}, gemm_tile22_kernel<5, 5, 3, 3>},
+    // 160 x 160: the N = 2560 projections (10 % less LDS traffic per output than 96 x 256); swapped operands,
+    // epilogue from registers
+    {{5, 5, 2, 2}, gemm_tile22_kernel<5, 5, 3, 3, true>},
     // 128 x 96 with a 5-deep ring: medium M (96-490 rows) over narrow N
     {{4, 3, 2, 2}, gemm_tile22_kernel<4, 3, 5, 5>},
     // 8 waves, two per SIMD: 256 x 256 and 256 x 224, the wide M = 2307 projections in under three rounds
