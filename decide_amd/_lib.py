@@ -50,6 +50,7 @@ class DhGemmPlan(ctypes.Structure):
         ("splits", c_uint32),
         ("workgroups", c_uint32),
         ("ws_bytes", c_uint64),
+        ("order", c_uint32),
     ]
 
 

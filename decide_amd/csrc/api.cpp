@@ -210,6 +210,12 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
   }
   a.nstripes = stripes;
   if (stripes == 0) return ok();  // N = 0: nothing to compute
+  if (!stream) {
+    dh::Plan po = p;
+    po.stripes = stripes;  // a grouped launch counts each member's own stripes
+    po.grid = p.mtiles * stripes * p.splits;
+    a.ngroup = dh::plan_order(po);
+  }
   const uint64_t grid64 = (uint64_t)p.mtiles * stripes * p.splits;
   if (grid64 > (uint64_t)INT32_MAX)
     return fail(DH_EINVAL, "gemm: %llu workgroups exceed one launch; split the call along M or N",
@@ -430,6 +436,7 @@ int dh_gemm_plan_for(const dh_ctx* ctx, uint32_t m, uint32_t n, uint32_t k, uint
   out->splits = p.splits;
   out->workgroups = p.grid;
   out->ws_bytes = p.ws_bytes;
+  out->order = dh::plan_order(p);
   return ok();
 }
 

@@ -36,6 +36,8 @@ struct TileArgs {
   uint32_t splits;    // split-K factor
   uint32_t kps;       // K per split (a multiple of kBK)
   uint32_t nstripes;  // column stripes summed over the members
+  uint32_t ngroup;    // work order within a split: 0 = M tiles fastest; g > 0 = the stripes in groups of g, and
+                      // within a group the stripes fastest, then the M tiles (see tile_coords in gemm_tile.hip)
   uint32_t count;     // members in use
   Member mem[kMaxMembers];
 };

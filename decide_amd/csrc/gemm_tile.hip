@@ -634,6 +634,31 @@ struct Pipe {
   }
 };
 
+// Work id -> (M tile, column stripe, K split). K splits are outermost. Within
+// a split, ngroup = 0 runs the M tiles fastest (consecutive ids share a
+// stripe's W); ngroup = g runs the stripes in groups of g, each group's stripes
+// fastest and then its M tiles, so that the contiguous run of ids one XCD gets
+// from xcd_remap covers a block of about (run / g) M tiles by g stripes: the
+// XCD's L2 then fetches fewer distinct X rows and W columns (the planner picks
+// g, plan.cpp). Every id below mtiles · nstripes · splits maps to a distinct
+// in-range triple: grp · g < nstripes, so gsz >= 1.
+__device__ __forceinline__ void tile_coords(const TileArgs& p, uint32_t wid, uint32_t& mt, uint32_t& gs,
+                                            uint32_t& split) {
+  const uint32_t per_split = p.mtiles * p.nstripes;
+  split = wid / per_split;
+  const uint32_t rem = wid - split * per_split;
+  if (p.ngroup == 0) {
+    mt = rem % p.mtiles;
+    gs = rem / p.mtiles;
+    return;
+  }
+  const uint32_t gw = p.mtiles * p.ngroup;
+  const uint32_t grp = rem / gw, local = rem - grp * gw;
+  const uint32_t gsz = min(p.ngroup, p.nstripes - grp * p.ngroup);
+  mt = local / gsz;
+  gs = grp * p.ngroup + local % gsz;
+}
+
 // One tile: FM x FN fragments per wave, WM waves along M and 4 / WM along N.
 template <int FM, int FN, int WM, int NBX, int NBW, bool SW = false>
 __device__ __forceinline__ void tile_body(const TileArgs& p) {
@@ -642,14 +667,8 @@ __device__ __forceinline__ void tile_body(const TileArgs& p) {
   constexpr int LDSB = P::LDS_BYTES > 64 * (BN + 4) * 4 ? P::LDS_BYTES : 64 * (BN + 4) * 4;
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
 
-  const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
-  // Work order: M tiles fastest, then column stripes, then K splits, so the
-  // consecutive work ids one XCD runs share one K range of X (and each
-  // stripe's W block is read by its M tiles back to back).
-  const uint32_t mt = wid % p.mtiles;
-  const uint32_t q = wid / p.mtiles;
-  const uint32_t gs = q % p.nstripes;
-  const uint32_t split = q / p.nstripes;
+  uint32_t mt, gs, split;
+  tile_coords(p, xcd_remap(blockIdx.x, gridDim.x), mt, gs, split);
   int mi = 0;
 #pragma unroll
   for (int i = 1; i < kMaxMembers; ++i)
@@ -1211,11 +1230,8 @@ void gemm_tile8_kernel(const TileArgs p) {
   static_assert(LDSB >= 128 * (BN + 4) * 4, "the epilogue's staging fits the rings");
   static_assert(LDSB >= BM * (BN / 2 + 8) * 2, "the fp16 SwiGLU staging fits the rings");
   __shared__ __attribute__((aligned(1024))) char lds[LDSB];
-  const uint32_t wid = xcd_remap(blockIdx.x, gridDim.x);
-  const uint32_t mt = wid % p.mtiles;
-  const uint32_t q = wid / p.mtiles;
-  const uint32_t gs = q % p.nstripes;
-  const uint32_t split = q / p.nstripes;
+  uint32_t mt, gs, split;
+  tile_coords(p, xcd_remap(blockIdx.x, gridDim.x), mt, gs, split);
   int mi = 0;
 #pragma unroll
   for (int i = 1; i < kMaxMembers; ++i)

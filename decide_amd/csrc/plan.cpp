@@ -10,7 +10,8 @@
 //     run in rounds of 256 (one per CU), the weights stream at most at
 //     6 TB/s, and split-K adds a reduction pass over S + 2 fp32 planes.
 // The table entry is used when the requested M is within 12 % of a measured
-// M for that (K, N); otherwise the model picks the variant and split.
+// M for that (K, N); otherwise the model picks the variant and split. Apart
+// from both, plan_order picks the tiles' work order for the XCDs' L2s.
 #include "plan.h"
 
 #include <algorithm>
@@ -306,6 +307,74 @@ Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count) {
     if (t < best_us) {
       best_us = t;
       best = plan_make(v, 1, m, n_total, k, 0u);
+    }
+  }
+  return best;
+}
+
+namespace {
+// Bytes-per-K of the distinct X tiles (bm rows each) and W stripes (bn columns
+// each) that work ids [a, b) of one split touch in the order of group width g.
+double span_cost(uint32_t a, uint32_t b, uint32_t mtiles, uint32_t nstripes, uint32_t g, double bm, double bn) {
+  if (a >= b) return 0.0;
+  if (g == 0) {
+    const uint32_t dm = std::min(b - a, mtiles), ds = (b - 1) / mtiles - a / mtiles + 1;
+    return dm * bm + ds * bn;
+  }
+  const uint32_t gw = mtiles * g;
+  double cost = 0.0;
+  for (uint32_t grp = a / gw; grp * gw < b; ++grp) {
+    const uint32_t gsz = std::min(g, nstripes - grp * g);
+    const uint32_t base = grp * gw, lo = std::max(a, base) - base, hi = std::min(b, base + mtiles * gsz) - base;
+    if (lo >= hi) continue;
+    const uint32_t ds = std::min(hi - lo, gsz), dm = (hi - 1) / gsz - lo / gsz + 1;
+    cost += dm * bm + ds * bn;
+  }
+  return cost;
+}
+
+double order_cost(const Plan& p, uint32_t g, double bm, double bn) {
+  constexpr uint32_t kXcds = 8, kSlots = 32;  // workgroups per XCD per round (one per CU)
+  const uint32_t per_split = p.mtiles * p.stripes, per = p.grid / kXcds, extra = p.grid % kXcds;
+  double cost = 0.0;
+  for (uint32_t x = 0; x < kXcds; ++x) {
+    const uint32_t start = x * per + std::min(x, extra), count = per + (x < extra ? 1u : 0u);
+    for (uint32_t j = 0; j < count; j += kSlots) {
+      uint32_t a = start + j;
+      const uint32_t b = start + std::min(count, j + kSlots);
+      while (a < b) {  // split boundaries: each split reads its own K range
+        const uint32_t s = a / per_split, e = std::min(b, (s + 1) * per_split);
+        cost += span_cost(a - s * per_split, e - s * per_split, p.mtiles, p.stripes, g, bm, bn);
+        a = e;
+      }
+    }
+  }
+  return cost;
+}
+
+int env_tile_group() {
+  static const int v = [] {
+    const char* e = std::getenv("DH_GEMM_TILE_GROUP");
+    return e && *e ? std::atoi(e) : -1;
+  }();
+  return v;
+}
+}  // namespace
+
+uint32_t plan_order(const Plan& p) {
+  if (p.variant == kStreamVariant || p.grid == 0) return 0;
+  if (env_tile_group() >= 0) return (uint32_t)env_tile_group();
+  if (p.mtiles < 2 || p.stripes < 2) return 0;
+  const VariantInfo v = variant_info(p.variant);
+  const double bm = v.bm(), bn = v.bn();
+  uint32_t best = 0;
+  double best_cost = order_cost(p, 0, bm, bn);
+  for (uint32_t g : {1u, 2u, 3u, 4u, 6u, 8u}) {
+    if (g >= p.stripes) break;
+    const double c = order_cost(p, g, bm, bn);
+    if (c < best_cost * 0.98) {  // a clear gain only: otherwise keep the M-fastest order
+      best_cost = c;
+      best = g;
     }
   }
   return best;

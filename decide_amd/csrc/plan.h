@@ -47,5 +47,13 @@ uint64_t plan_ws_need(uint32_t max_m, uint32_t n, uint32_t k, uint64_t max_ws);
 // Best plan for a grouped launch of `count` members of widths ns[] that share
 // X (no split-K). Each member rounds up to whole column stripes of its own.
 Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count);
+// The tile kernels' work order for plan p (TileArgs::ngroup): the hardware
+// deals workgroups to the 8 XCDs round-robin and xcd_remap gives each XCD a
+// contiguous run of work ids, so the order decides which X row blocks and W
+// column stripes share one XCD's L2. Returns the stripe-group width (0 = M
+// tiles fastest) that minimises the bytes of distinct X and W tiles each XCD
+// fetches per round of one workgroup per CU, over a few candidates.
+// DH_GEMM_TILE_GROUP=<g> in the environment fixes it (for measurements).
+uint32_t plan_order(const Plan& p);
 
 }  // namespace dh

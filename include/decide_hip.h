@@ -97,6 +97,9 @@ typedef struct dh_gemm_plan {
   uint32_t splits;      /* split-K factor (1 = none) */
   uint32_t workgroups;  /* grid size of the tile kernel */
   uint64_t ws_bytes;    /* split-K workspace the launch needs */
+  uint32_t order;       /* work order of the tile kernel: 0 = M tiles fastest; g > 0 = column stripes in groups of
+                           g, each group's stripes fastest (chosen per launch so that each XCD's L2 sees a compact
+                           block of X rows and W columns); the outputs are the same bits whatever the order */
 } dh_gemm_plan;
 
 /* --- context (decide: Gemm::new / Gemm::with_impl, kernels/gemm.rs:56-83;

@@ -159,6 +159,23 @@ def test_planner_invariants_on_random_shapes():
         assert p["workgroups"] == -(-m // p["bm"]) * -(-n // p["bn"]) * p["splits"], name
         assert p["ws_bytes"] == (p["splits"] * m * n * 4 if p["splits"] > 1 else 0), name
         assert p["ws_bytes"] <= 512 << 20, name
+        # the work order: M tiles fastest, or column stripes in groups narrower than the stripe count
+        assert p["order"] in (0, 1, 2, 3, 4, 6, 8), name
+        assert p["order"] == 0 or p["order"] < -(-n // p["bn"]), name
+        if p["variant"] == _lib.DH_GEMM_STREAM_VARIANT:
+            assert p["order"] == 0, name
+
+
+def test_tile_order_gives_each_xcd_a_compact_block():
+    """The 8 XCDs each take a contiguous run of work ids. At M = 2,307 the down and out projections make
+    15 x 16 tiles of 160 x 160 (30 per XCD): in M-fastest order each XCD's run covers all 15 row blocks of X
+    and 2 column stripes of W (17 tile loads per XCD), in groups of 6 stripes 5 row blocks x 6 stripes (11; on the
+    two XCDs that share the last group, of 4 stripes, 8 row blocks x 4 stripes: 12).
+    At M = 603 the 4 row blocks per stripe already make compact runs, and the order stays M-fastest."""
+    assert plan_for(2307, 2560, 9216, Epilogue.AddF32)["order"] == 6
+    assert plan_for(2307, 2560, 4096, Epilogue.AddF32)["order"] == 6
+    for n, k in ((18432, 2560), (12352, 2560), (2560, 9216)):
+        assert plan_for(603, n, k, Epilogue.StoreF32)["order"] == 0, (n, k)
 
 
 @pytest.mark.parametrize("m", [1, 4, 603, 2307])

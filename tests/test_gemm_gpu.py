@@ -427,6 +427,28 @@ def test_config4_projections_m2307(gpu, kernels, stream, kn):
     check_gemm(f"C4 k{k} n{n}", got[rows], want)
 
 
+# One shape per tile work order the planner picks (dh_gemm_plan.order: 0 = M tiles fastest, g = column stripes
+# in groups of g), each a single planned launch without split-K.
+ORDER_SHAPES = {0: (603, 18432, 2560), 2: (800, 2048, 2560), 3: (2000, 2048, 2560), 4: (1500, 2560, 4096),
+                6: (2307, 2560, 4096), 8: (1024, 3072, 1024)}
+
+
+@pytest.mark.parametrize("order", sorted(ORDER_SHAPES))
+def test_every_tile_order_is_exact(gpu, kernels, stream, order):
+    """The work order only decides which workgroup computes which tile, so every tile must still be computed
+    once, in place: integer-valued fp16 in [-4, 4] make every partial sum an integer below 2^24, so the fp32
+    result is exact whatever the order (the f64 product is the exact answer)."""
+    m, n, k = ORDER_SHAPES[order]
+    p = kernels.gemm.plan(m, n, k, Epilogue.StoreF32)
+    assert p["order"] == order and p["splits"] == 1, p
+    rng = np.random.default_rng(order)
+    x = rng.integers(-4, 5, (m, k)).astype(np.float16)
+    w = rng.integers(-4, 5, (n, k)).astype(np.float16)
+    want = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+    got = run_gemm(kernels, stream, x, w, Epilogue.StoreF32)
+    assert np.array_equal(got, want), f"order {order}: {int((got != want).sum())} outputs differ"
+
+
 def random_shapes(count: int, seed: int):
     """Seeded shapes across the planner's range: M from 1 (the weight-streaming kernel) to ~1300, N and K
     any multiple of 32 (so K % 64 == 32 leaves a half stage, split-K included), row strides padded past
