@@ -130,11 +130,14 @@ struct PrepSrc {
   uint32_t ldp;
 };
 
-// Raw conv input row s of channel c (s < 0: the conv state; s ≥ T: zero).
-__device__ __forceinline__ float raw_at(const PrepSrc& in, int s, uint32_t T, uint32_t c) {
-  if (s < 0) return in.prev[(size_t)(3 + s) * convk::CONV_DIM + c];
-  return (uint32_t)s < T ? in.p[(size_t)s * in.ldp + c] : 0.f;
+// Where raw conv input row s of channels c, c + 1 (c even) is read from: the conv state for s < 0, else row
+// s of p clamped into 0 .. T - 1 (T >= 1), so that the load needs no branch; rows s >= T are zeroed by the
+// caller after the load (raw_zero).
+__device__ __forceinline__ const f2* raw_ptr(const PrepSrc& in, int s, uint32_t T, uint32_t c) {
+  return (const f2*)(s < 0 ? in.prev + (size_t)(3 + s) * convk::CONV_DIM + c
+                           : in.p + (size_t)min((uint32_t)s, T - 1) * in.ldp + c);
 }
+__device__ __forceinline__ f2 raw_zero(f2 x, int s, uint32_t T) { return s < 0 || (uint32_t)s < T ? x : f2{0.f, 0.f}; }
 
 // ---------------------------------------------------------------------------
 // prep: one workgroup per (chunk, key head). The Gram tiles Q Kᵀ and K Kᵀ are
@@ -163,13 +166,24 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
   __shared__ __attribute__((aligned(16))) float Lg[2][C], Bt[2][C], Gm[2][C], SCw[2][C], Rh[2][C];
   __shared__ float Ysc[8 * 16 * 17];  // per-wave 16 × 16 scratch of the blocked inversion
   const uint32_t c = blockIdx.x, hk = blockIdx.y, t0 = c * C;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: per-head values load into SGPRs
   const int r = lane & 15, g = lane >> 4;
   const int hh = wave >> 2, lw = wave & 3;  // this wave's value head (of the key head's two), and its wave in that half
   const uint32_t h = 2 * hk + hh;
   float* const ATs = R2 + hh * kAT;  // A[i][j] at [i][j], T[i][j] at [j][i] (see above)
   float* const out0 = ws + ((size_t)c * NV + 2 * hk) * kWsStride;
   float* const out = out0 + hh * kWsStride;
+  // Waves 0 and 4 form value head h's gates after their conv step; their loads go out first, so that the
+  // latency overlaps the conv (rows past T read row T - 1 and are dropped below).
+  float ga = 0.f, gb = 0.f;
+  if (lw == 0) {
+    const size_t ta = (size_t)min(t0 + (uint32_t)lane, T - 1) * ldab + h;
+    ga = a[ta];
+    gb = b[ta];
+  }
+  // Waves 0 and 4 form value head h's gates after their conv step; their loads go out first, so that the
+  // latency overlaps the conv (rows past T read row T - 1 and are dropped below).
 
   if constexpr (FUSED) {
     // wave w: k (w < 4) or q (w ≥ 4) of key head hk over the chunk's rows 16 (w & 3) .. + 16, lane l owning
@@ -179,15 +193,11 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
     const uint32_t c = (uint32_t)(isq ? hk : NK + hk) * DK + 2 * lane;
     const f4 w0 = *(const f4*)(src.convw + (size_t)c * 4), w1 = *(const f4*)(src.convw + (size_t)(c + 1) * 4);
     const int tr0 = (int)t0 + 16 * run;
-    f2 x[19];  // raw rows tr0 - 3 .. tr0 + 15, all loads in flight together
+    f2 x[19];  // raw rows tr0 - 3 .. tr0 + 15, all loads in flight together (no branch between them)
 #pragma unroll
-    for (int j = 0; j < 19; ++j) {
-      const int s = tr0 - 3 + j;
-      if (s < 0)
-        x[j] = *(const f2*)(src.prev + (size_t)(3 + s) * convk::CONV_DIM + c);
-      else
-        x[j] = (uint32_t)s < T ? *(const f2*)(src.p + (size_t)s * src.ldp + c) : f2{0.f, 0.f};
-    }
+    for (int j = 0; j < 19; ++j) x[j] = *raw_ptr(src, tr0 - 3 + j, T, c);
+#pragma unroll
+    for (int j = 0; j < 19; ++j) x[j] = raw_zero(x[j], tr0 - 3 + j, T);
     float* dst = isq ? R2 : Ks;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
@@ -209,8 +219,8 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
     const uint32_t t = t0 + lane;
     float lam = 0.f, bt = 0.f;
     if (t < T) {
-      lam = -expf(a_log[h]) * softplus_p(a[(size_t)t * ldab + h] + dt_bias[h]);
-      bt = 1.0f / (1.0f + expf(-b[(size_t)t * ldab + h]));
+      lam = -expf(a_log[h]) * softplus_p(ga + dt_bias[h]);
+      bt = 1.0f / (1.0f + expf(-gb));
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {  // inclusive prefix sum of log g over the chunk
@@ -229,7 +239,10 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
 
   // The 20 Gram tiles: tile t < 10 is block t of Q Kᵀ (lower triangle incl. diagonal), t ≥ 10 block t − 10 of
   // K Kᵀ (strictly lower); wave w takes t = w, w + 8, w + 16. Each tile then gives both value heads' M
-  // (γ_i/γ_j, to global; blocks above the diagonal written as zeros) or A (β_i γ_i/γ_j, over Q's LDS).
+  // (γ_i/γ_j, to global; the scan reads only the blocks on and below the diagonal) or A (β_i γ_i/γ_j, over Q's
+  // LDS). The K rows go in as the MFMA's A operand, so lane (r, g) ends with the tile's row r and columns
+  // 4 g .. 4 g + 3 (the same products summed in the same order as with the operands the other way round) and
+  // stores them as one 16-byte piece.
   f4 gacc[3];
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
@@ -237,7 +250,7 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
     if (tt < 20) {
       int ti, tj;
       lower_block(tt < 10 ? tt : tt - 10, ti, tj);
-      gacc[u] = nt_tile<DK>((tt < 10 ? R2 : Ks) + 16 * ti * LDF, LDF, Ks + 16 * tj * LDF, LDF, r, g,
+      gacc[u] = nt_tile<DK>(Ks + 16 * tj * LDF, LDF, (tt < 10 ? R2 : Ks) + 16 * ti * LDF, LDF, r, g,
                             f4{0.f, 0.f, 0.f, 0.f});
     }
   }
@@ -249,23 +262,22 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
       const bool isq = tt < 10;
       int ti, tj;
       lower_block(isq ? tt : tt - 10, ti, tj);
-      const int j = 16 * tj + r;
+      const int i = 16 * ti + r, j0 = 16 * tj + 4 * g;
 #pragma unroll
-      for (int vh = 0; vh < 2; ++vh)
+      for (int vh = 0; vh < 2; ++vh) {
+        f4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int i = 16 * ti + 4 * g + e;
+          const int j = j0 + e;
           const float rr = i >= j ? expf(Lg[vh][i] - Lg[vh][j]) : 0.f;
-          if (!isq)
-            R2[vh * kAT + i * LDT + j] = i > j ? Bt[vh][i] * rr * gacc[u][e] : 0.f;
-          else
-            out0[vh * kWsStride + kOffM + i * C + j] = rr * gacc[u][e];
+          v[e] = isq ? rr * gacc[u][e] : (i > j ? Bt[vh][i] * rr * gacc[u][e] : 0.f);
         }
+        if (isq)
+          *(f4*)(out0 + vh * kWsStride + kOffM + i * C + j0) = v;
+        else
+          *(f4*)(R2 + vh * kAT + i * LDT + j0) = v;
+      }
     }
-  }
-  for (int e = tid; e < 2 * C * C; e += 512) {
-    const int f = e & (C * C - 1);
-    if ((f & 63) >> 4 > f >> 10) out0[(e >> 12) * kWsStride + kOffM + f] = 0.f;
   }
   {  // K̃ᵀ[d][j] = (γ_C/γ_j) K[j][d] for the scan; threads 0-255 for value head 2 hk, 256-511 for 2 hk + 1
     const int vh = tid >> 8, t8 = tid & 255;
@@ -280,29 +292,32 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
   }
   if (tid < 2 * C) out0[(tid >> 6) * kWsStride + kOffGam + (tid & 63)] = Gm[tid >> 6][tid & 63];
 
-  // This wave's U operand, V[t0 + 16 jb + 4 g + s][16 (2 lw + q2) + r], straight into registers; the loads
-  // run during the inversion below (fused: its 4 tokens' 7 raw rows per block, conv + SiLU in registers).
+  // This wave's U operand, V[t0 + 16 jb + 4 g + s][32 lw + 2 r + q2] (its U tile q2 takes the head's value
+  // channels 32 lw + 2 ρ + q2, so each lane holds two adjacent channels and loads them as one 8-byte piece),
+  // straight into registers; the loads run during the inversion below (fused: its 4 tokens' 7 raw rows per
+  // block, conv + SiLU in registers).
   f4 vr[2][4];
-  f4 vw[2];          // fused: the conv weights of this wave's two value channels
-  float vx[2][4][7];  // fused: raw rows 16 jb + 4 g - 3 .. + 3 of them, combined after the inversion
+  f4 vw[2];       // fused: the conv weights of this lane's two value channels
+  f2 vx[4][7];    // fused: raw rows 16 jb + 4 g - 3 .. + 3 of them, combined after the inversion
+  const uint32_t cv = 32 * lw + 2 * r;  // this lane's first value channel in the head
+  if constexpr (FUSED) {
+    const uint32_t c = 2 * convk::KEY_DIM + h * DV + cv;
+    vw[0] = *(const f4*)(src.convw + (size_t)c * 4);
+    vw[1] = *(const f4*)(src.convw + (size_t)(c + 1) * 4);
 #pragma unroll
-  for (int q2 = 0; q2 < 2; ++q2) {
-    if constexpr (FUSED) {
-      const uint32_t c = 2 * convk::KEY_DIM + h * DV + 16 * (2 * lw + q2) + r;
-      vw[q2] = *(const f4*)(src.convw + (size_t)c * 4);
+    for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
+      for (int j = 0; j < 7; ++j) vx[jb][j] = *raw_ptr(src, (int)t0 + 16 * jb + 4 * g - 3 + j, T, c);
+  } else {
 #pragma unroll
-        for (int j = 0; j < 7; ++j) vx[q2][jb][j] = raw_at(src, (int)t0 + 16 * jb + 4 * g - 3 + j, T, c);
-    } else {
+    for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          const uint32_t t = t0 + 16 * jb + 4 * g + s4;
-          vr[q2][jb][s4] = t < T ? src.v[((size_t)t * NV + h) * DV + 16 * (2 * lw + q2) + r] : 0.f;
-        }
-    }
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const uint32_t t = t0 + 16 * jb + 4 * g + s4;
+        const f2 x = *(const f2*)(src.v + ((size_t)min(t, T - 1) * NV + h) * DV + cv);  // clamped: no branch
+        vr[0][jb][s4] = t < T ? x[0] : 0.f;
+        vr[1][jb][s4] = t < T ? x[1] : 0.f;
+      }
   }
 
   // T = (I + A)⁻¹ per value head, blocked 4 × 4 over 16 × 16 blocks. Diagonal blocks by forward
@@ -361,49 +376,64 @@ delta_chunk_prep_kernel(const PrepSrc src, const float* __restrict__ a,
       for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
-          const float* x = vx[q2][jb];
-          vr[q2][jb][s4] = t0 + 16 * jb + 4 * g + s4 < T ? convk::conv_silu(vw[q2], x[s4], x[s4 + 1], x[s4 + 2], x[s4 + 3])
-                                                         : 0.f;
+          // raw rows past T enter only outputs of tokens past T, which are zero
+          const f2* x = vx[jb];
+          vr[q2][jb][s4] = t0 + 16 * jb + 4 * g + s4 < T
+                               ? convk::conv_silu(vw[q2], x[s4][q2], x[s4 + 1][q2], x[s4 + 2][q2], x[s4 + 3][q2])
+                               : 0.f;
         }
   }
 
-  // W = T diag(βγ) K and U = T diag(β) V. Wave lw of the head's half: key/value columns 16 td for td = 2 lw,
-  // 2 lw + 1. T is lower triangular, so row block ti sums over token blocks jb ≤ ti; within a block lane
-  // group g holds tokens 16 jb + 4 g .. + 4 (one ds_read_b128 of T and of the scale), and the B operand
-  // K[j][16 td + r] is conflict-free with the row stride of 132 floats (V's comes from registers).
+  // W = T diag(βγ) K and U = T diag(β) V. Wave lw of the head's half: key/value channels 32 lw .. + 32, as two
+  // 16-channel tiles q2 (W: channels 32 lw + 16 q2 + ρ; U: 32 lw + 2 ρ + q2, the order its operand was loaded
+  // in). T is lower triangular, so row block ti sums over token blocks jb ≤ ti; within a block lane group g
+  // holds tokens 16 jb + 4 g .. + 4 (one ds_read_b128 of the scale; K[j][32 lw + 16 q2 + r] is conflict-free
+  // with the row stride of 132 floats, V's comes from registers). The channels go in as the MFMA's A operand,
+  // so lane (r, g) ends with token row 16 ti + r and 4 channels of each tile (the same products summed in the
+  // same order as with the operands the other way round), which it stores as 16-byte pieces: W's 4 adjacent
+  // channels per tile, and U's 8 adjacent channels of both tiles, interleaved.
 #pragma unroll
   for (int isu = 0; isu < 2; ++isu) {
     const float* sc = isu ? Bt[hh] : SCw[hh];
     float* dst = out + (isu ? kOffU : kOffW);
+    sfor<0, 4>([&](auto tic) {
+      constexpr int ti = decltype(tic)::value;
+      f4 tv[ti + 1];  // T[16 ti + r][16 jb + 4 g + s] · scale
 #pragma unroll
-    for (int q2 = 0; q2 < 2; ++q2) {
-      const int d0 = 16 * (2 * lw + q2);
-      sfor<0, 4>([&](auto tic) {
-        constexpr int ti = decltype(tic)::value;
-        f4 ta[ti + 1], sv[ti + 1], rb[ti + 1];
+      for (int jb = 0; jb <= ti; ++jb) {
+        const f4 sv = *(const f4*)(sc + 16 * jb + 4 * g);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) tv[jb][s] = ATs[(16 * jb + 4 * g + s) * LDT + 16 * ti + r] * sv[s];
+      }
+      f4 acc[2];
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) {
+        f4 rb[ti + 1];
 #pragma unroll
         for (int jb = 0; jb <= ti; ++jb) {
-#pragma unroll
-          for (int s = 0; s < 4; ++s)  // T[16 ti + r][16 jb + 4 g + s]
-            ta[jb][s] = ATs[(16 * jb + 4 * g + s) * LDT + 16 * ti + r];
-          sv[jb] = *(const f4*)(sc + 16 * jb + 4 * g);
           if (isu) {
             rb[jb] = vr[q2][jb];
           } else {
 #pragma unroll
-            for (int s = 0; s < 4; ++s) rb[jb][s] = Ks[(16 * jb + 4 * g + s) * LDF + d0 + r];
+            for (int s = 0; s < 4; ++s) rb[jb][s] = Ks[(16 * jb + 4 * g + s) * LDF + 32 * lw + 16 * q2 + r];
           }
         }
         __builtin_amdgcn_sched_barrier(0);
-        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+        acc[q2] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int jb = 0; jb <= ti; ++jb)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) acc = mfma4(ta[jb][s] * sv[jb][s], rb[jb][s], acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(16 * ti + 4 * g + e) * DK + d0 + r] = acc[e];
-      });
-    }
+          for (int s = 0; s < 4; ++s) acc[q2] = mfma4(rb[jb][s], tv[jb][s], acc[q2]);
+      }
+      float* row = dst + (16 * ti + r) * DK + 32 * lw;
+      if (isu) {
+        *(f4*)(row + 8 * g) = f4{acc[0][0], acc[1][0], acc[0][1], acc[1][1]};
+        *(f4*)(row + 8 * g + 4) = f4{acc[0][2], acc[1][2], acc[0][3], acc[1][3]};
+      } else {
+        *(f4*)(row + 4 * g) = acc[0];
+        *(f4*)(row + 16 + 4 * g) = acc[1];
+      }
+    });
   }
 }
 
