@@ -335,11 +335,12 @@ double span_cost(uint32_t a, uint32_t b, uint32_t mtiles, uint32_t nstripes, uin
 
 double order_cost(const Plan& p, uint32_t g, double bm, double bn) {
   constexpr uint32_t kXcds = 8, kSlots = 32;  // workgroups per XCD per round (one per CU)
+  constexpr uint32_t kRounds = 4;  // rounds counted per XCD: later ones repeat the pattern, and this bounds host time
   const uint32_t per_split = p.mtiles * p.stripes, per = p.grid / kXcds, extra = p.grid % kXcds;
   double cost = 0.0;
   for (uint32_t x = 0; x < kXcds; ++x) {
     const uint32_t start = x * per + std::min(x, extra), count = per + (x < extra ? 1u : 0u);
-    for (uint32_t j = 0; j < count; j += kSlots) {
+    for (uint32_t j = 0; j < count && j < kRounds * kSlots; j += kSlots) {
       uint32_t a = start + j;
       const uint32_t b = start + std::min(count, j + kSlots);
       while (a < b) {  // split boundaries: each split reads its own K range
@@ -365,6 +366,15 @@ uint32_t plan_order(const Plan& p) {
   if (p.variant == kStreamVariant || p.grid == 0) return 0;
   if (env_tile_group() >= 0) return (uint32_t)env_tile_group();
   if (p.mtiles < 2 || p.stripes < 2) return 0;
+  // a forward plans the same few shapes in every layer: the last answers per thread, keyed by what they depend on
+  struct Memo {
+    int variant = -1;
+    uint32_t mtiles = 0, stripes = 0, splits = 0, order = 0;
+  };
+  thread_local Memo memo[8];
+  Memo& mo = memo[(p.mtiles * 31u + p.stripes * 7u + p.splits * 3u + (uint32_t)p.variant) & 7u];
+  if (mo.variant == p.variant && mo.mtiles == p.mtiles && mo.stripes == p.stripes && mo.splits == p.splits)
+    return mo.order;
   const VariantInfo v = variant_info(p.variant);
   const double bm = v.bm(), bn = v.bn();
   uint32_t best = 0;
@@ -377,6 +387,7 @@ uint32_t plan_order(const Plan& p) {
       best = g;
     }
   }
+  mo = Memo{p.variant, p.mtiles, p.stripes, p.splits, best};
   return best;
 }
 
