@@ -210,17 +210,17 @@ int launch_plan(dh_ctx* c, hipStream_t s, const dh::Plan& p, const void* x, uint
   }
   a.nstripes = stripes;
   if (stripes == 0) return ok();  // N = 0: nothing to compute
-  if (!stream) {
-    dh::Plan po = p;
-    po.stripes = stripes;  // a grouped launch counts each member's own stripes
-    po.grid = p.mtiles * stripes * p.splits;
-    a.ngroup = dh::plan_order(po);
-  }
   const uint64_t grid64 = (uint64_t)p.mtiles * stripes * p.splits;
   if (grid64 > (uint64_t)INT32_MAX)
     return fail(DH_EINVAL, "gemm: %llu workgroups exceed one launch; split the call along M or N",
                 (unsigned long long)grid64);
   const uint32_t grid = (uint32_t)grid64;
+  if (!stream) {
+    dh::Plan po = p;
+    po.stripes = stripes;  // a grouped launch counts each member's own stripes
+    po.grid = grid;
+    a.ngroup = dh::plan_order(po);
+  }
   if (p.splits > 1) {
     if (count != 1) return fail(DH_EINVAL, "gemm: split-K needs a single member");
     if (fixed_ws) {
