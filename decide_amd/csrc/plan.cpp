@@ -353,10 +353,15 @@ double order_cost(const Plan& p, uint32_t g, double bm, double bn) {
   return cost;
 }
 
+// DH_GEMM_TILE_GROUP=<g>: -1 (unset, or not a number in 0..64) lets the planner choose; 0..64 fixes the order
+// (widths past a launch's stripe count act as one group; the cap keeps mtiles · g far from wrapping in the kernel).
 int env_tile_group() {
   static const int v = [] {
     const char* e = std::getenv("DH_GEMM_TILE_GROUP");
-    return e && *e ? std::atoi(e) : -1;
+    if (!e || !*e) return -1;
+    char* end = nullptr;
+    const long g = std::strtol(e, &end, 10);
+    return *end == '\0' && g >= 0 && g <= 64 ? (int)g : -1;
   }();
   return v;
 }

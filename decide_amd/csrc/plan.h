@@ -53,7 +53,7 @@ Plan plan_grouped(uint32_t m, uint32_t k, const uint32_t* ns, uint32_t count);
 // column stripes share one XCD's L2. Returns the stripe-group width (0 = M
 // tiles fastest) that minimises the bytes of distinct X and W tiles each XCD
 // fetches per round of one workgroup per CU, over a few candidates.
-// DH_GEMM_TILE_GROUP=<g> in the environment fixes it (for measurements).
+// DH_GEMM_TILE_GROUP=<g> (0..64) in the environment fixes it (for measurements).
 uint32_t plan_order(const Plan& p);
 
 }  // namespace dh
