@@ -11,7 +11,9 @@ import ctypes
 import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_uint16, c_uint32, c_uint64, c_void_p
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdecide_hip.so")
+# DH_LIB names another build of the same library (the sanitizer builds of decide_amd/csrc/Makefile); unset, the
+# in-tree library is the one loaded.
+LIB_PATH = os.environ.get("DH_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdecide_hip.so")
 
 DH_OK = 0
 DH_EINVAL = 1
