@@ -16,7 +16,8 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
-ORACLE_SO = os.path.join(ORACLE_DIR, "liboracle.so")
+# DH_ORACLE_LIB names another build of the checker (oracle/Makefile's `sanitized` target); unset, the in-tree one
+ORACLE_SO = os.environ.get("DH_ORACLE_LIB") or os.path.join(ORACLE_DIR, "liboracle.so")
 
 _lib = None
 
