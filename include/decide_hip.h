@@ -99,7 +99,9 @@ typedef struct dh_gemm_plan {
   uint64_t ws_bytes;    /* split-K workspace the launch needs */
   uint32_t order;       /* work order of the tile kernel: 0 = M tiles fastest; g > 0 = column stripes in groups of
                            g, each group's stripes fastest (chosen per launch so that each XCD's L2 sees a compact
-                           block of X rows and W columns); the outputs are the same bits whatever the order */
+                           block of X rows and W columns); the outputs are the same bits whatever the order. The
+                           environment variable DH_GEMM_TILE_GROUP=<g> (0..64), read once per process, fixes it
+                           for every launch (for measurements; the library reads no other variable) */
 } dh_gemm_plan;
 
 /* --- context (decide: Gemm::new / Gemm::with_impl, kernels/gemm.rs:56-83;
